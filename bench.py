@@ -1,0 +1,275 @@
+"""Benchmark of the gfx950 GQA attention hot path (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads ...]
+
+A step is one pass of the attention hot path over one batch of synthetic,
+seeded inputs already resident in HBM:
+  prefill  K-Norm + RoPE row kernel (K-hat), then the fused prefill kernel
+           (Q-Norm + RoPE on load, causal GQA FlashAttention forward);
+  decode   append of the new token's K-hat/V into the cache, then the split-K
+           decode kernel (+ its merge) over ragged lengths.
+The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
+(B8 S2048 Hq16 Hkv8 D128 causal bf16); FLOPs are the algorithmic
+4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
+prefill kernel's own FLOPs by its average duration from HIP events recorded
+on its launch stream.  ``secondary`` holds the other workloads, each with its
+roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2).  ``cpu_baseline``
+times the oracle (fp32 torch on the host cores) on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "prefill attn TFLOP/s (% bf16 MFMA peak); decode KV GB/s (% HBM peak)"
+YARN = {"type": "yarn", "factor": 4.0, "original_max_position_embeddings": 32768}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _randn(shape, seed, device, dtype=torch.bfloat16, cpu=True):
+    if cpu:
+        g = torch.Generator().manual_seed(seed)
+        return torch.randn(*shape, generator=g).to(dtype).to(device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    return torch.randn(*shape, generator=g, device=device, dtype=dtype)
+
+
+class Prefill:
+    kind = "prefill"
+
+    def __init__(self, nq, name, B, S, Hq, Hkv, D, seed, rope_scaling=None, wscale=0.02,
+                 device="cuda", cpu_gen=True):
+        self.nq, self.name = nq, name
+        self.B, self.S, self.Hq, self.Hkv, self.D = B, S, Hq, Hkv, D
+        # projections' (B, S, H, D) storage viewed as (B, H, S, D), as in the model
+        self.q = _randn((B, S, Hq, D), seed, device, cpu=cpu_gen).transpose(1, 2)
+        self.k = _randn((B, S, Hkv, D), seed + 100, device, cpu=cpu_gen).transpose(1, 2)
+        self.v = _randn((B, S, Hkv, D), seed + 200, device, cpu=cpu_gen).transpose(1, 2)
+        g = torch.Generator().manual_seed(seed + 300)
+        self.qw = (1 + wscale * torch.randn(D, generator=g)).to(device)
+        self.kw = (1 + wscale * torch.randn(D, generator=g)).to(device)
+        cos, sin = nq.build_tables(D, S, 1e6, rope_scaling)
+        self.cos, self.sin = cos.to(device), sin.to(device)
+        self.khat = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
+        self.out = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
+        self.work = 4.0 * D * B * Hq * S * (S + 1) / 2
+        self.rope_scaling = rope_scaling
+
+    def step(self, ev=None):
+        nq = self.nq
+        nq.qk_norm_rope(k=self.k, k_out=self.khat, k_weight=self.kw, eps=1e-6, cos=self.cos,
+                        sin=self.sin)
+        if ev is not None:
+            ev[0].record()
+        nq.attention_prefill(self.q, self.khat, self.v, q_weight=self.qw, eps=1e-6, cos=self.cos,
+                             sin=self.sin, causal=True, out=self.out)
+        if ev is not None:
+            ev[1].record()
+
+    def describe(self):
+        return {"workload": self.name, "batch": self.B, "seq_len": self.S, "num_heads": self.Hq,
+                "num_kv_heads": self.Hkv, "head_dim": self.D, "causal": True,
+                "rope": "yarn x4" if self.rope_scaling else "theta 1e6"}
+
+    def roofline(self, kernel_ms, traffic=None):
+        ach = self.work / (kernel_ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "kernel": "prefill_kernel", "kernel_ms": round(kernel_ms, 5)}
+
+    def throughput(self, step_ms):
+        return self.work / (step_ms * 1e-3) / 1e12, "TFLOP/s"
+
+
+class Decode:
+    kind = "decode"
+
+    def __init__(self, nq, name, B, Hq, Hkv, D, Tcap, seed, device="cuda"):
+        self.nq, self.name = nq, name
+        self.B, self.Hq, self.Hkv, self.D, self.Tcap = B, Hq, Hkv, D, Tcap
+        g = torch.Generator().manual_seed(seed)
+        self.lens_cpu = torch.randint(1024, Tcap + 1, (B,), generator=g, dtype=torch.int32)
+        self.lens = self.lens_cpu.to(device)
+        self.row = (self.lens_cpu - 1).to(device)            # slot of the new token
+        self.max_len = int(self.lens_cpu.max())
+        gd = torch.Generator(device=device).manual_seed(seed)
+        self.kc = torch.randn(B, Hkv, Tcap, D, generator=gd, device=device, dtype=torch.bfloat16)
+        self.vc = torch.randn(B, Hkv, Tcap, D, generator=gd, device=device, dtype=torch.bfloat16)
+        self.q = _randn((B, Hq, 1, D), seed + 1, device)
+        self.knew = _randn((B, Hkv, 1, D), seed + 2, device)
+        self.vnew = _randn((B, Hkv, 1, D), seed + 3, device)
+        self.w = torch.ones(D, device=device)
+        cos, sin = nq.build_tables(D, Tcap, 1e6)
+        self.cos, self.sin = cos.to(device), sin.to(device)
+        self.out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
+        nbytes = nq.decode_workspace_bytes(B, Hq, D, self.max_len)
+        self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        self.work = float(2 * Hkv * D * 2 * int(self.lens_cpu.sum()) + 2 * B * Hq * D * 2)
+
+    def step(self, ev=None):
+        nq = self.nq
+        nq.qk_norm_rope(k=self.knew, v=self.vnew, k_out=self.kc, v_out=self.vc, k_weight=self.w,
+                        eps=1e-6, cos=self.cos, sin=self.sin, pos_base=self.row,
+                        kv_row_base=self.row)
+        if ev is not None:
+            ev[0].record()
+        nq.attention_decode(self.q, self.kc, self.vc, self.lens, max_len=self.max_len,
+                            q_weight=self.w, eps=1e-6, cos=self.cos, sin=self.sin, out=self.out,
+                            workspace=self.ws)
+        if ev is not None:
+            ev[1].record()
+
+    def describe(self):
+        return {"workload": self.name, "batch": self.B, "num_heads": self.Hq,
+                "num_kv_heads": self.Hkv, "head_dim": self.D, "cache_capacity": self.Tcap,
+                "kv_lens": "U[1024, %d], sum %d" % (self.Tcap, int(self.lens_cpu.sum()))}
+
+    def roofline(self, kernel_ms, traffic=None):
+        ach = self.work / (kernel_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "kernel": "decode_split_kernel + decode_merge_kernel", "kernel_ms": round(kernel_ms, 5)}
+
+    def throughput(self, step_ms):
+        return self.work / (step_ms * 1e-3) / 1e9, "GB/s"
+
+
+def time_workload(w, steps, warmup):
+    for _ in range(warmup):
+        w.step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        w.step(evs[i])
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    kernel_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    avg_kernel = sum(kernel_ms) / len(kernel_ms)
+    return wall_ms / steps, avg_kernel, kernel_ms[len(kernel_ms) // 2]
+
+
+def cpu_baseline(budget_s=15.0):
+    """The oracle (fp32 torch on the host) on the same Qwen3-1.7B-like prefill shape.
+
+    Sample: whole batch rows of B8 S2048 Hq16 Hkv8 D128, run row by row until
+    ~budget_s of CPU time is spent; FLOPs counted as on the GPU.
+    """
+    from oracle import attention_path
+    threads = torch.get_num_threads()
+    B, S, Hq, Hkv, D = 8, 2048, 16, 8, 128
+    g = torch.Generator().manual_seed(1001)
+    q = torch.randn(1, Hq, S, D, generator=g)
+    k = torch.randn(1, Hkv, S, D, generator=g)
+    v = torch.randn(1, Hkv, S, D, generator=g)
+    w = 1 + 0.02 * torch.randn(D, generator=g)
+    from nano_qwen_amd.rope import build_tables
+    cos, sin = build_tables(D, S, 1e6)
+    pos = torch.arange(S)
+    rows, t0 = 0, time.perf_counter()
+    while rows < B:
+        attention_path(q, k, v, q_weight=w, k_weight=w, eps=1e-6, cos=cos, sin=sin, q_pos=pos,
+                       causal=True)
+        rows += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    flops = 4.0 * D * rows * Hq * S * (S + 1) / 2
+    return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{rows} of 8 batch rows of B8 S2048 Hq16 Hkv8 D128 causal prefill "
+                      f"(QK-Norm+RoPE+GQA attention, fp32 torch oracle), {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workloads", default="c2,c3,c4,c5",
+                    help="comma list of c2 (headline), c3, c4, c5")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the attention hot path is built and measured on a "
+              "single MI355X (no collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import nano_qwen_amd as nq
+    dev = "cuda"
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+    names = [w.strip() for w in args.workloads.split(",") if w.strip()]
+    if "c2" not in names:
+        names.insert(0, "c2")
+
+    def build(name):
+        if name == "c2":
+            return Prefill(nq, "Qwen3-1.7B-like attention prefill B8 S2048 Hq16 Hkv8 D128 causal bf16",
+                           8, 2048, 16, 8, 128, seed=1001)
+        if name == "c3":
+            return Prefill(nq, "Qwen3-8B-like attention prefill B4 S8192 Hq32 Hkv8 D128 causal bf16, "
+                           "fused QK-Norm+RoPE", 4, 8192, 32, 8, 128, seed=1002)
+        if name == "c4":
+            return Decode(nq, "Qwen3-235B-A22B decode B64 Hq64 Hkv4 D128, ragged KV cache bf16",
+                          64, 64, 4, 128, 32768, seed=1003)
+        if name == "c5":
+            return Prefill(nq, "YaRN long-context prefill B1 S131072 Hq32 Hkv4 D128 causal bf16",
+                           1, 131072, 32, 4, 128, seed=1004, rope_scaling=YARN, cpu_gen=False)
+        raise SystemExit(f"unknown workload {name}")
+
+    results = {}
+    for name in names:
+        w = build(name)
+        steps = args.steps if name != "c5" else max(2, min(args.steps, 4))
+        warm = args.warmup if name != "c5" else 1
+        log(f"{name}: {steps} timed steps after {warm} warmup")
+        step_ms, kern_ms, kern_med = time_workload(w, steps, warm)
+        val, unit = w.throughput(step_ms)
+        results[name] = (w, step_ms, kern_ms, kern_med, val, unit, steps, warm)
+        log(f"{name}: {step_ms:.4f} ms/step, kernel avg {kern_ms:.4f} ms, {val:.2f} {unit}")
+        if name != "c2":
+            del w
+            torch.cuda.empty_cache()
+
+    w, step_ms, kern_ms, kern_med, val, unit, steps, warm = results["c2"]
+    line = {
+        "metric": METRIC, "value": round(val, 3), "unit": unit, "n_gpus": 1,
+        "steps": steps, "warmup": warm, "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, QK-Norm weights 1+0.02*N(0,1))",
+        "config": w.describe(),
+        "roofline": w.roofline(kern_ms),
+    }
+    sec = {}
+    for name, (w2, sms, kms, kmed, v2, u2, st2, wu2) in results.items():
+        if name == "c2":
+            continue
+        sec[name] = {"config": w2.describe(), "value": round(v2, 3), "unit": u2,
+                     "ms_per_step": round(sms, 5), "steps": st2, "roofline": w2.roofline(kms)}
+    line["secondary"] = sec
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle on host cores)")
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * nq_attn.h -- C ABI of the gfx950 (MI355X) GQA attention library
+ * (libnqattn.so), a drop-in for nano-qwen's attention hot path.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor pointers are HIP device pointers; the caller owns every
+ *     buffer (including the decode workspace).  Nothing here allocates,
+ *     frees or synchronises.  Launches go on `stream` (a hipStream_t; NULL =
+ *     the default stream).
+ *   - A "row" is head_dim contiguous elements.  4-D tensors are described by
+ *     their base pointer plus three element strides for the (batch, head,
+ *     sequence) axes; the head_dim axis must be contiguous.  Base pointers must
+ *     be 16-byte aligned and strides multiples of 16 bytes.
+ *   - dtype codes: NQ_DTYPE_BF16 (bfloat16 stored as 16-bit words) or
+ *     NQ_DTYPE_F32.  Matrix products run on bf16 MFMA with fp32 accumulation;
+ *     norm, RoPE and softmax arithmetic is fp32.
+ *   - head_dim must be 64 or 128.  num_heads % num_kv_heads == 0 and query head
+ *     h reads kv head h / (num_heads / num_kv_heads).
+ *   - cos/sin tables are fp32 (max_pos, head_dim/2) row-major, as built by the
+ *     reference's RotaryEmbedding (plain RoPE or YaRN).  Positions outside
+ *     [0, max_pos) are clamped into the table.
+ *   - Return value: NQ_OK (0) on success, a positive NQ_ERR_* code for an
+ *     argument error, or a negative value -(hipError_t) for a launch error.
+ *     nq_last_error() returns a thread-local message for the last failure.
+ */
+#ifndef NQ_ATTN_H_
+#define NQ_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NQ_OK 0
+#define NQ_ERR_INVALID 1
+#define NQ_ERR_UNSUPPORTED 2
+#define NQ_ERR_WORKSPACE 3
+
+#define NQ_DTYPE_BF16 0
+#define NQ_DTYPE_F32 1
+
+/* Library version, e.g. 100 for 0.1.0. */
+int nq_version(void);
+
+/* Thread-local text of the last error ("" when the last call succeeded). */
+const char* nq_last_error(void);
+
+/*
+ * QK-Norm + RoPE over rows of Q and K, plus an optional row copy of V.
+ *
+ * Replaces model/norm.py:17-22 (RMSNorm as QK-Norm, applied at
+ * model/attention.py:95-97), model/rope.py:133-161 (apply_rotary_pos_emb) and
+ * kernels/rope.py:99-108 (apply_rope: in-place when q_out == q, k_out == k),
+ * and the concatenation in KVCache.update (model/attention.py:31-38): K and V
+ * rows land at destination row kv_row_base[b] + s of a preallocated
+ * (B, Hkv, T_cap, D) cache.
+ *
+ * q, k, v: source rows (any of them NULL to skip that job), with strides
+ *   {batch, head, seq} in elements; Q has Hq heads, K and V have Hkv heads.
+ * q_out/k_out/v_out: destinations with their strides; Q rows land at row s.
+ * q_weight/k_weight: fp32 RMSNorm weights (D), NULL = no norm (qk_norm=False).
+ * cos_tab/sin_tab: fp32 RoPE tables, NULL = no rotation (norm or copy only).
+ * eps: RMSNorm epsilon (config.rms_norm_eps).
+ * pos: int32 (B, S) positions, or NULL to use pos_base[b] + s, or with
+ *   pos_base NULL too, pos0 + s (pos0 = 0 is the reference's
+ *   position_ids=None, model/rope.py:123-126).
+ * kv_row_base: int32 (B) cache row offsets for K/V, or NULL to use kv_row0.
+ */
+int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
+                    const int64_t* q_out_strides, const void* k, const int64_t* k_strides,
+                    void* k_out, const int64_t* k_out_strides, const void* v,
+                    const int64_t* v_strides, void* v_out, const int64_t* v_out_strides,
+                    int B, int S, int Hq, int Hkv, int D, int dtype_in, int dtype_out,
+                    const float* q_weight, const float* k_weight, float eps,
+                    const float* cos_tab, const float* sin_tab, int max_pos,
+                    const int32_t* pos, const int32_t* pos_base, int pos0,
+                    const int32_t* kv_row_base, int kv_row0, void* stream);
+
+/*
+ * Causal / full GQA prefill attention (FlashAttention-2 style forward).
+ *
+ * Replaces kernels/flash_attn.py:130-143 (flash_attention) and the
+ * post-projection part of Attention.forward, model/attention.py:95-115:
+ * QK-Norm and RoPE on Q are fused into the Q load (when q_weight or cos_tab is
+ * given), the K/V operands are used as stored (for the reference path, K is
+ * already normalised and rotated by nq_qk_norm_rope, V raw), the GQA
+ * expansion of attention.py:106-108 is implicit, and SDPA is replaced.
+ *
+ * q: (B, Hq, S, D) with strides q_strides; k, v: (B, Hkv, T, D); o: output
+ *   (B, Hq, S, D) with strides o_strides (pass the strides of a
+ *   (B, S, Hq, D) buffer to get o_proj's input layout directly).
+ * lse: optional fp32 (B, Hq, S) natural-log sum-exp of the scaled scores.
+ * q_weight: RMSNorm weight for Q (NULL = none); cos_tab/sin_tab: RoPE table
+ *   for Q (NULL = none); q_pos / q_pos_base / q_pos0: Q positions as in
+ *   nq_qk_norm_rope.
+ * causal: query i sees key j iff j <= i + (T - S) (top-left == bottom-right
+ *   when S == T, which is SDPA's is_causal in the reference).
+ * sm_scale <= 0 selects 1/sqrt(D), SDPA's default (attention.py:110).
+ * Requires 128 % (Hq / Hkv) == 0 and S <= T when causal.
+ */
+int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
+                        const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                        void* o, const int64_t* o_strides, float* lse, int B, int Hq, int Hkv,
+                        int S, int T, int D, int dtype, const float* q_weight, float eps,
+                        const float* cos_tab, const float* sin_tab, int max_pos,
+                        const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
+                        int causal, float sm_scale, void* stream);
+
+/*
+ * Bytes of fp32 workspace nq_attn_decode_fwd needs for these sizes.
+ * max_len bounds every lens[b]; chunk is the number of keys per split
+ * (0 selects the library default).
+ */
+int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int D, int max_len, int chunk);
+
+/*
+ * Single-token decode attention against a ragged KV cache (split-K).
+ *
+ * Replaces model/attention.py:95-115 at S == 1 with a KVCache: the new
+ * token's Q is QK-Normed and rotated in the kernel (q_weight / cos_tab may be
+ * NULL), then attends keys [0, lens[b]) of the cache with no causal mask
+ * (attention.py:113 sets is_causal=False whenever a cache is present).
+ *
+ * q: (B, Hq, D) with strides {batch, head}; k_cache/v_cache: (B, Hkv, T_cap, D)
+ *   with strides {batch, head, seq}, holding post-norm post-RoPE K and raw V.
+ * lens: int32 (B), 1 <= lens[b] <= max_len <= T_cap (the kernel clamps to
+ *   max_len); NULL = every row has max_len keys.
+ * q_pos: int32 (B) RoPE positions of the query token; NULL = q_pos0 for
+ *   every row, or lens[b] - 1 when q_pos0 < 0.
+ * o: output (B, Hq, D) with strides {batch, head}.
+ * workspace: device buffer of at least
+ *   nq_attn_decode_workspace_bytes(B, Hq, D, max_len, chunk) bytes.
+ * Requires Hq / Hkv <= 16 or a multiple of 16.
+ */
+int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const void* k_cache,
+                       const int64_t* k_strides, const void* v_cache, const int64_t* v_strides,
+                       const int32_t* lens, void* o, const int64_t* o_strides, void* workspace,
+                       int64_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_len,
+                       int chunk, int dtype, const float* q_weight, float eps,
+                       const float* cos_tab, const float* sin_tab, int max_pos,
+                       const int32_t* q_pos, int q_pos0, float sm_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NQ_ATTN_H_ */

@@ -1,0 +1,27 @@
+"""nano-qwen's GQA attention hot path on MI355X (gfx950), as a drop-in.
+
+QK-Norm, RoPE/YaRN, causal FlashAttention-2-style prefill and split-K
+single-token decode against a KV cache, as hand-written HIP kernels in
+libnqattn.so (C ABI in include/nq_attn.h), called from PyTorch-ROCm through
+ctypes.  Build with ``python -m nano_qwen_amd.build``.
+
+Public surface, mirroring the reference:
+  Attention, KVCache           model/attention.py:24-118
+  RMSNorm                      model/norm.py:11-22
+  RotaryEmbedding, apply_rotary_pos_emb   model/rope.py:78-161
+  flash_attention, apply_rope  kernels/flash_attn.py:130, kernels/rope.py:99
+  AttentionConfig              attention fields of model/config.py:14-83
+"""
+
+from .config import AttentionConfig
+from .ops import (apply_rope, attention_decode, attention_prefill, decode_workspace_bytes,
+                  flash_attention, qk_norm_rope)
+from .norm import RMSNorm
+from .rope import RotaryEmbedding, apply_rotary_pos_emb, build_tables
+from .attention import Attention, KVCache, stats
+
+__all__ = [
+    "Attention", "KVCache", "RMSNorm", "RotaryEmbedding", "AttentionConfig",
+    "apply_rotary_pos_emb", "build_tables", "flash_attention", "apply_rope",
+    "qk_norm_rope", "attention_prefill", "attention_decode", "decode_workspace_bytes", "stats",
+]

@@ -1,0 +1,256 @@
+"""Drop-in GQA attention and KV cache for nano-qwen (model/attention.py:24-118).
+
+``Attention`` keeps the reference's constructor, submodule names (so state
+dicts load unchanged: ``q_proj``, ``k_proj``, ``v_proj``, ``o_proj``,
+``q_norm``, ``k_norm``) and ``forward(hidden_states, position_ids=None,
+attention_mask=None, kv_cache=None)`` signature.  ``KVCache`` keeps
+``update(key, value) -> (K, V)``, ``seq_len`` and ``reset()`` and the
+(B, Hkv, T, D) layout, but stores rows in a preallocated buffer instead of
+concatenating on every step.
+
+Dispatch (following kernels/flash_attn.py:139's convention):
+  * device tensors, no attention_mask, no autograd -> gfx950 kernels:
+    one row-kernel launch (K-Norm + RoPE -> K-hat, plus the V copy when a
+    cache is used), then the prefill kernel (Q-Norm + RoPE fused into the Q
+    load), or the split-K decode kernel when a cache is present and S == 1;
+  * autograd or an explicit attention_mask -> torch ops on the device, the
+    reference's own arithmetic (SDPA), since the kernels are forward-only and
+    maskless;
+  * host tensors -> RuntimeError (the kernels are the product; there is no
+    CPU path).
+
+Reference semantics reproduced by default (quirks of the reference, kept for
+parity, each switchable):
+  * ``position_ids=None`` rotates at positions 0..S-1 even when a cache
+    already holds rows (model/rope.py:123-126).  ``rope_positions="cache"``
+    continues from the cache length instead.
+  * A forward with a cache is not causal (attention.py:113), so a multi-token
+    prefill into a cache is bidirectional.  ``cache_prefill_causal=True``
+    makes it causal.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .config import num_kv_groups
+from .norm import RMSNorm
+from .rope import RotaryEmbedding
+
+# Counters of which path forward() took (kernel launches vs torch fallback).
+stats = {"kernel_forward": 0, "torch_forward": 0}
+
+
+class KVCache:
+    """Preallocated (B, Hkv, T_cap, D) cache with the reference's API.
+
+    ``key``/``value`` are views of the valid rows (B, Hkv, seq_len, D), like
+    the tensors the reference's KVCache holds.  Capacity grows by doubling
+    when an update does not fit (one copy); pass ``max_seq_len`` to size it
+    once.
+    """
+
+    def __init__(self, max_seq_len: Optional[int] = None):
+        self.max_seq_len = max_seq_len
+        self._k: Optional[torch.Tensor] = None
+        self._v: Optional[torch.Tensor] = None
+        self._len = 0
+        self.key: Optional[torch.Tensor] = None
+        self.value: Optional[torch.Tensor] = None
+
+    @property
+    def seq_len(self) -> int:
+        return self._len
+
+    @property
+    def capacity(self) -> int:
+        return 0 if self._k is None else self._k.shape[2]
+
+    def reserve(self, B: int, H: int, total: int, D: int, dtype, device) -> None:
+        """Make room for ``total`` rows (allocating or growing the storage)."""
+        if self._k is not None:
+            if (self._k.shape[0], self._k.shape[1], self._k.shape[3]) != (B, H, D):
+                raise ValueError(f"cache holds {tuple(self._k.shape)}, update needs B={B} H={H} D={D}")
+            if self._k.dtype != dtype or self._k.device != torch.device(device):
+                raise TypeError("cache dtype/device differ from the update")
+            if total <= self.capacity:
+                return
+        cap = max(total, self.max_seq_len or 0, 2 * self.capacity, 64)
+        cap = (cap + 63) // 64 * 64
+        k = torch.empty(B, H, cap, D, dtype=dtype, device=device)
+        v = torch.empty(B, H, cap, D, dtype=dtype, device=device)
+        if self._len:
+            k[:, :, :self._len] = self._k[:, :, :self._len]
+            v[:, :, :self._len] = self._v[:, :, :self._len]
+        self._k, self._v = k, v
+        self._refresh()
+
+    def storage(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        return self._k, self._v
+
+    def advance(self, n: int) -> None:
+        self._len += n
+        self._refresh()
+
+    def _refresh(self) -> None:
+        if self._k is None:
+            self.key = self.value = None
+        else:
+            self.key = self._k[:, :, :self._len]
+            self.value = self._v[:, :, :self._len]
+
+    def update(self, key: torch.Tensor, value: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Append (B, Hkv, S, D) rows; returns all valid rows (attention.py:31-38)."""
+        B, H, S, D = key.shape
+        self.reserve(B, H, self._len + S, D, key.dtype, key.device)
+        self._k[:, :, self._len:self._len + S] = key
+        self._v[:, :, self._len:self._len + S] = value
+        self.advance(S)
+        return self.key, self.value
+
+    def reset(self) -> None:
+        self._len = 0
+        self._refresh()
+
+
+class Attention(nn.Module):
+    """Multi-head attention with GQA and QK-Norm (model/attention.py:49-118)."""
+
+    def __init__(self, config, layer_idx: int = 0):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.hidden_size = config.hidden_size
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.num_kv_groups = num_kv_groups(config)
+        bias = getattr(config, "attention_bias", False)
+        self.q_proj = nn.Linear(self.hidden_size, self.num_heads * self.head_dim, bias=bias)
+        self.k_proj = nn.Linear(self.hidden_size, self.num_kv_heads * self.head_dim, bias=bias)
+        self.v_proj = nn.Linear(self.hidden_size, self.num_kv_heads * self.head_dim, bias=bias)
+        self.o_proj = nn.Linear(self.num_heads * self.head_dim, self.hidden_size, bias=bias)
+        self.qk_norm = getattr(config, "qk_norm", True)
+        if self.qk_norm:
+            self.q_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+            self.k_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+        self.rotary_emb = RotaryEmbedding(
+            dim=self.head_dim,
+            max_position_embeddings=config.max_position_embeddings,
+            base=config.rope_theta,
+            rope_scaling=getattr(config, "rope_scaling", None),
+        )
+        dropout = getattr(config, "attention_dropout", 0.0)
+        self.attn_dropout = nn.Dropout(dropout) if dropout > 0 else nn.Identity()
+        self.rope_positions = "reference"     # or "cache"
+        self.cache_prefill_causal = False
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, hidden_states: torch.Tensor, position_ids: Optional[torch.Tensor] = None,
+                attention_mask: Optional[torch.Tensor] = None,
+                kv_cache: Optional[KVCache] = None) -> torch.Tensor:
+        if not hidden_states.is_cuda:
+            raise RuntimeError("nano_qwen_amd.Attention runs on HIP devices only")
+        B, S, _ = hidden_states.shape
+        H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        q = self.q_proj(hidden_states)
+        k = self.k_proj(hidden_states)
+        v = self.v_proj(hidden_states)
+        dropout = self.training and getattr(self.config, "attention_dropout", 0.0) > 0
+        needs_grad = q.requires_grad or k.requires_grad or v.requires_grad
+        if attention_mask is not None or needs_grad or dropout:
+            stats["torch_forward"] += 1
+            return self._torch_forward(q, k, v, position_ids, attention_mask, kv_cache)
+        stats["kernel_forward"] += 1
+
+        q4 = q.view(B, S, H, D).transpose(1, 2)
+        k4 = k.view(B, S, Hkv, D).transpose(1, 2)
+        v4 = v.view(B, S, Hkv, D).transpose(1, 2)
+        cos, sin = self.rotary_emb.tables_f32()
+        qw = self.q_norm.weight if self.qk_norm else None
+        kw = self.k_norm.weight if self.qk_norm else None
+        eps = self.config.rms_norm_eps
+        past = kv_cache.seq_len if kv_cache is not None else 0
+        pos_offset = past if (self.rope_positions == "cache" and position_ids is None) else 0
+
+        if kv_cache is None:
+            k_hat = torch.empty(B, S, Hkv, D, dtype=k.dtype, device=k.device).transpose(1, 2)
+            ops.qk_norm_rope(k=k4, k_out=k_hat, k_weight=kw, eps=eps, cos=cos, sin=sin,
+                             position_ids=position_ids, pos_offset=pos_offset)
+            o = ops.attention_prefill(q4, k_hat, v4, q_weight=qw, eps=eps, cos=cos, sin=sin,
+                                      position_ids=position_ids, pos_offset=pos_offset, causal=True)
+            return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
+
+        kv_cache.reserve(B, Hkv, past + S, D, k.dtype, k.device)
+        kc, vc = kv_cache.storage()
+        ops.qk_norm_rope(k=k4, v=v4, k_out=kc, v_out=vc, k_weight=kw, eps=eps, cos=cos, sin=sin,
+                         position_ids=position_ids, pos_offset=pos_offset, kv_row_offset=past)
+        kv_cache.advance(S)
+        T = past + S
+        if S == 1:
+            qp = None
+            if position_ids is not None:
+                qp = position_ids.reshape(B, -1)[:, 0]
+            o = ops.attention_decode(q4, kc, vc, None, max_len=T, q_weight=qw, eps=eps, cos=cos,
+                                     sin=sin, q_pos=qp, q_pos0=pos_offset)
+            return self.o_proj(o.reshape(B, 1, H * D))
+        o = ops.attention_prefill(q4, kc[:, :, :T], vc[:, :, :T], q_weight=qw, eps=eps, cos=cos,
+                                  sin=sin, position_ids=position_ids, pos_offset=pos_offset,
+                                  causal=self.cache_prefill_causal)
+        return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
+
+    # ------------------------------------------------------------- torch path
+    def _torch_forward(self, q, k, v, position_ids, attention_mask, kv_cache):
+        """The reference's own arithmetic (attention.py:91-118) for autograd / masks."""
+        B, S, _ = q.shape
+        H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        q = q.view(B, S, H, D).transpose(1, 2)
+        k = k.view(B, S, Hkv, D).transpose(1, 2)
+        v = v.view(B, S, Hkv, D).transpose(1, 2)
+        if self.qk_norm:
+            q = _rms(q, self.q_norm.weight, self.config.rms_norm_eps)
+            k = _rms(k, self.k_norm.weight, self.config.rms_norm_eps)
+        past = kv_cache.seq_len if kv_cache is not None else 0
+        if position_ids is None and self.rope_positions == "cache" and past:
+            position_ids = torch.arange(past, past + S, device=q.device)[None].expand(B, S)
+        cos, sin = self.rotary_emb(q, position_ids)
+        q, k = _rotate(q, cos, sin), _rotate(k, cos, sin)
+        if kv_cache is not None:
+            k, v = kv_cache.update(k, v)
+        G = self.num_kv_groups
+        if G > 1:
+            k = k.repeat_interleave(G, dim=1)
+            v = v.repeat_interleave(G, dim=1)
+        causal = attention_mask is None and (kv_cache is None or (self.cache_prefill_causal and S > 1))
+        T = k.shape[2]
+        mask, is_causal = attention_mask, False
+        if causal and T == S:
+            is_causal = True
+        elif causal:
+            # bottom-right aligned causal mask for queries appended after T - S cached rows
+            mask = torch.ones(S, T, dtype=torch.bool, device=q.device).tril(diagonal=T - S)
+        o = F.scaled_dot_product_attention(
+            q, k, v, attn_mask=mask, is_causal=is_causal,
+            dropout_p=self.config.attention_dropout if self.training else 0.0)
+        o = o.transpose(1, 2).contiguous().view(B, S, -1)
+        return self.o_proj(o)
+
+
+def _rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).type_as(x) * w
+
+
+def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    if cos.dim() == 2:
+        cos, sin = cos[None, None], sin[None, None]
+    else:
+        cos, sin = cos[:, None], sin[:, None]
+    x1, x2 = x[..., :half], x[..., half:]
+    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)

@@ -1,0 +1,103 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Storage types are bf16 (clang __bf16) or fp32; all arithmetic that is not
+// an MFMA runs in fp32.  Vector loads are 16 bytes per lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nq {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------- MFMA
+// v_mfma_f32_32x32x16_bf16: A 32x16, B 16x32, C/D 32x32 fp32.
+//   A: lane l holds row (l % 32), k = (l / 32) * 8 + [0, 8)
+//   B: lane l holds col (l % 32), k = (l / 32) * 8 + [0, 8)
+//   D: lane l holds col (l % 32), rows (i / 4) * 8 + (l / 32) * 4 + (i % 4), i < 16
+__device__ __forceinline__ floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_16x16x32_bf16: A 16x32, B 32x16, C/D 16x16 fp32.
+//   A: lane l holds row (l % 16), k = (l / 16) * 8 + [0, 8)
+//   B: lane l holds col (l % 16), k = (l / 16) * 8 + [0, 8)
+//   D: lane l holds col (l % 16), rows (l / 16) * 4 + i, i < 4
+__device__ __forceinline__ floatx4 mfma16(bf16x8 a, bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- loads
+// 8 consecutive elements starting at p (16-byte aligned for bf16, 32 for fp32).
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16> {
+  __device__ __forceinline__ static floatx8 load_f32(const bf16* p) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+    return __builtin_convertvector(v, floatx8);
+  }
+  __device__ __forceinline__ static bf16x8 load_bf16(const bf16* p) {
+    return *reinterpret_cast<const bf16x8*>(p);
+  }
+};
+template <> struct Vec8<float> {
+  __device__ __forceinline__ static floatx8 load_f32(const float* p) {
+    floatx4 a = *reinterpret_cast<const floatx4*>(p);
+    floatx4 b = *reinterpret_cast<const floatx4*>(p + 4);
+    return floatx8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  }
+  __device__ __forceinline__ static bf16x8 load_bf16(const float* p) {
+    return __builtin_convertvector(load_f32(p), bf16x8);
+  }
+};
+
+__device__ __forceinline__ bf16x8 to_bf16x8(floatx8 v) { return __builtin_convertvector(v, bf16x8); }
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, floatx8 v);
+template <>
+__device__ __forceinline__ void store8<bf16>(bf16* p, floatx8 v) {
+  *reinterpret_cast<bf16x8*>(p) = __builtin_convertvector(v, bf16x8);
+}
+template <>
+__device__ __forceinline__ void store8<float>(float* p, floatx8 v) {
+  *reinterpret_cast<floatx4*>(p) = floatx4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<floatx4*>(p + 4) = floatx4{v[4], v[5], v[6], v[7]};
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, floatx4 v);
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* p, floatx4 v) {
+  *reinterpret_cast<bf16x4*>(p) = __builtin_convertvector(v, bf16x4);
+}
+template <>
+__device__ __forceinline__ void store4<float>(float* p, floatx4 v) {
+  *reinterpret_cast<floatx4*>(p) = v;
+}
+
+// ---------------------------------------------------------------- lanes
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Position of (b, s): explicit positions win, else base[b] + s, else pos0 + s.
+__device__ __forceinline__ int row_position(const int32_t* pos, const int32_t* pos_base, int pos0,
+                                            int b, int s, int S) {
+  if (pos) return pos[(int64_t)b * S + s];
+  return (pos_base ? pos_base[b] : pos0) + s;
+}
+
+__device__ __forceinline__ int clamp_pos(int p, int max_pos) {
+  return p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+}
+
+}  // namespace nq

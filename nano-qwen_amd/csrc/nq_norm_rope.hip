@@ -1,0 +1,177 @@
+// Row kernel: RMSNorm over head_dim + rotate-half RoPE from an fp32 table,
+// written to an arbitrary strided destination (a KV-cache slot or a buffer).
+//
+// Replaces, for the attention path of nano-qwen:
+//   model/norm.py:17-22           RMSNorm used as QK-Norm (attention.py:95-97)
+//   model/rope.py:133-161         apply_rotary_pos_emb (rotate-half pairing)
+//   kernels/rope.py:99-108        apply_rope (in-place when src == dst)
+//   model/attention.py:31-38      KVCache.update (rows land at row_base[b] + s)
+//
+// One launch processes up to three jobs (Q, K, V); V rows are copied (and
+// converted) without arithmetic.  Layout: a row is D contiguous elements;
+// (b, h, s) strides are free.  A row of D elements is handled by D/8 lanes,
+// each owning 8 consecutive elements (one 16-byte bf16 load).  The norm's
+// sum of squares is reduced across those lanes with xor shuffles; the RoPE
+// partner of element d (d + D/2) lives in the lane D/16 positions away.
+// HBM-bound: one read and one write per element, table reads hit L2.
+
+#include "nq_common.hpp"
+#include "nq_internal.hpp"
+
+namespace nq {
+
+struct RowJob {
+  const void* src;
+  void* dst;
+  int64_t sb, sh, ss;   // source strides (elements)
+  int64_t db, dh, ds;   // destination strides (elements)
+  const float* weight;  // RMSNorm weight (D) or null
+  int H;
+  int rope;             // apply RoPE
+  int norm;             // apply RMSNorm
+  int use_row_base;     // destination row = row_base[b] + s
+};
+
+struct RowParams {
+  RowJob job[3];
+  int njobs;
+  int B, S, D;
+  float eps;
+  const float* cos_tab;
+  const float* sin_tab;
+  int max_pos;
+  const int32_t* pos;
+  const int32_t* pos_base;
+  int pos0;
+  const int32_t* row_base;
+  int row0;
+};
+
+template <typename TI, typename TO, int D>
+__global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
+  constexpr int LPR = D / 8;          // lanes per row
+  constexpr int RPW = 64 / LPR;       // rows per wave
+  constexpr int RPB = RPW * 4;        // rows per 256-thread block
+  const RowJob& jb = p.job[blockIdx.y];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane % LPR;         // 8-element chunk within the row
+  const int64_t row = (int64_t)blockIdx.x * RPB + wave * RPW + lane / LPR;
+  const int64_t nrows = (int64_t)p.B * jb.H * p.S;
+  const bool active = row < nrows;
+  // row -> (b, h, s) with s fastest
+  const int64_t rr = active ? row : 0;
+  const int s = (int)(rr % p.S);
+  const int h = (int)((rr / p.S) % jb.H);
+  const int b = (int)(rr / ((int64_t)p.S * jb.H));
+
+  const TI* src = reinterpret_cast<const TI*>(jb.src) + b * jb.sb + h * jb.sh + s * jb.ss + sub * 8;
+  floatx8 x = active ? Vec8<TI>::load_f32(src) : floatx8{0, 0, 0, 0, 0, 0, 0, 0};
+
+  if (jb.norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+    const float r = rsqrtf(ss / (float)D + p.eps);
+    floatx8 w = Vec8<float>::load_f32(jb.weight + sub * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = x[e] * r * w[e];
+  }
+  if (jb.rope) {
+    const int pos = clamp_pos(row_position(p.pos, p.pos_base, p.pos0, b, s, p.S), p.max_pos);
+    const int half_lanes = LPR / 2;
+    const bool first = sub < half_lanes;
+    const int dd = (sub % half_lanes) * 8;
+    floatx8 c = Vec8<float>::load_f32(p.cos_tab + (int64_t)pos * (D / 2) + dd);
+    floatx8 sn = Vec8<float>::load_f32(p.sin_tab + (int64_t)pos * (D / 2) + dd);
+    floatx8 y;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float partner = shfl_xor_f(x[e], half_lanes);
+      // first half: x1*c - x2*s ; second half: x2*c + x1*s
+      y[e] = first ? (x[e] * c[e] - partner * sn[e]) : (x[e] * c[e] + partner * sn[e]);
+    }
+    x = y;
+  }
+  if (!active) return;
+  const int drow = jb.use_row_base ? ((p.row_base ? p.row_base[b] : p.row0) + s) : s;
+  TO* dst = reinterpret_cast<TO*>(jb.dst) + b * jb.db + h * jb.dh + (int64_t)drow * jb.ds + sub * 8;
+  store8<TO>(dst, x);
+}
+
+template <typename TI, typename TO, int D>
+static hipError_t launch_rows(const RowParams& p, int max_h, hipStream_t st) {
+  constexpr int RPB = (64 / (D / 8)) * 4;
+  const int64_t nrows = (int64_t)p.B * max_h * p.S;
+  dim3 grid((unsigned)((nrows + RPB - 1) / RPB), (unsigned)p.njobs);
+  hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
+                               const int64_t* q_out_strides, const void* k,
+                               const int64_t* k_strides, void* k_out,
+                               const int64_t* k_out_strides, const void* v,
+                               const int64_t* v_strides, void* v_out,
+                               const int64_t* v_out_strides, int B, int S, int Hq, int Hkv,
+                               int D, int dtype_in, int dtype_out, const float* q_weight,
+                               const float* k_weight, float eps, const float* cos_tab,
+                               const float* sin_tab, int max_pos, const int32_t* pos,
+                               const int32_t* pos_base, int pos0,
+                               const int32_t* kv_row_base, int kv_row0, void* stream) {
+  nq_clear_error();
+  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (B <= 0 || S <= 0) return nq_fail(NQ_ERR_INVALID, "B and S must be positive (B=%d S=%d)", B, S);
+  if (!nq_dtype_ok(dtype_in) || !nq_dtype_ok(dtype_out))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "dtype codes must be NQ_DTYPE_BF16 or NQ_DTYPE_F32");
+  if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
+    return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
+  const int esz_in = nq_dtype_size(dtype_in), esz_out = nq_dtype_size(dtype_out);
+  RowParams p{};
+  p.B = B; p.S = S; p.D = D; p.eps = eps;
+  p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
+  p.pos = pos; p.pos_base = pos_base; p.pos0 = pos0;
+  p.row_base = kv_row_base; p.row0 = kv_row0;
+  int nj = 0, max_h = 0;
+  struct In { const void* s; const int64_t* ss; void* d; const int64_t* ds; int H; const float* w; int rope; int rb; const char* name; };
+  In ins[3] = {{q, q_strides, q_out, q_out_strides, Hq, q_weight, 1, 0, "q"},
+               {k, k_strides, k_out, k_out_strides, Hkv, k_weight, 1, 1, "k"},
+               {v, v_strides, v_out, v_out_strides, Hkv, nullptr, 0, 1, "v"}};
+  for (const In& in : ins) {
+    if (!in.s) continue;
+    if (!in.d || !in.ss || !in.ds) return nq_fail(NQ_ERR_INVALID, "%s: output and strides required", in.name);
+    if (in.H <= 0) return nq_fail(NQ_ERR_INVALID, "%s: head count must be positive", in.name);
+    if (!nq_aligned16(in.s) || !nq_aligned16(in.d))
+      return nq_fail(NQ_ERR_INVALID, "%s: base pointers must be 16-byte aligned", in.name);
+    for (int i = 0; i < 3; ++i) {
+      if ((in.ss[i] * esz_in) % 16 || (in.ds[i] * esz_out) % 16)
+        return nq_fail(NQ_ERR_INVALID, "%s: strides must be multiples of 16 bytes", in.name);
+    }
+    RowJob& j = p.job[nj++];
+    j.src = in.s; j.dst = in.d;
+    j.sb = in.ss[0]; j.sh = in.ss[1]; j.ss = in.ss[2];
+    j.db = in.ds[0]; j.dh = in.ds[1]; j.ds = in.ds[2];
+    j.weight = in.w; j.H = in.H; j.rope = in.rope && cos_tab != nullptr; j.norm = in.w != nullptr;
+    j.use_row_base = in.rb;
+    if (in.H > max_h) max_h = in.H;
+  }
+  if (nj == 0) return NQ_OK;
+  p.njobs = nj;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  const bool bi = dtype_in == NQ_DTYPE_BF16, bo = dtype_out == NQ_DTYPE_BF16;
+#define NQ_ROWS(TI, TO)                                                               \
+  e = (D == 128) ? launch_rows<TI, TO, 128>(p, max_h, st) : launch_rows<TI, TO, 64>(p, max_h, st)
+  if (bi && bo) NQ_ROWS(bf16, bf16);
+  else if (bi && !bo) NQ_ROWS(bf16, float);
+  else if (!bi && bo) NQ_ROWS(float, bf16);
+  else NQ_ROWS(float, float);
+#undef NQ_ROWS
+  return nq_check_launch(e);
+}

@@ -1,0 +1,343 @@
+"""torch-facing wrappers over the gfx950 attention kernels (libnqattn.so).
+
+Tensors are passed to the C ABI as raw device pointers plus element strides;
+the kernels never allocate.  Every function here requires HIP device tensors
+and raises if the library is missing -- there is no CPU or eager fallback.
+
+Mirrors of the reference's kernel-level API (kernels/flash_attn.py:130-143,
+kernels/rope.py:99-108) keep their names and argument meaning:
+``flash_attention(q, k, v, causal=True, sm_scale=None)`` and
+``apply_rope(q, k, cos, sin)`` (in place).  The fused entry points used by the
+drop-in ``Attention`` module are ``qk_norm_rope``, ``attention_prefill`` and
+``attention_decode``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "qk_norm_rope",
+    "attention_prefill",
+    "attention_decode",
+    "decode_workspace_bytes",
+    "flash_attention",
+    "apply_rope",
+]
+
+_DTYPES = {torch.bfloat16: _lib.NQ_DTYPE_BF16, torch.float32: _lib.NQ_DTYPE_F32}
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; the kernels take bfloat16 or float32") from None
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("nano_qwen_amd attention kernels need HIP device tensors "
+                               f"(got a tensor on {t.device}); there is no CPU path")
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    es = t.element_size()
+    if t.data_ptr() % 16:
+        return False
+    if t.stride(-1) != 1:
+        return False
+    return all((s * es) % 16 == 0 for s in t.stride()[:-1])
+
+
+def _rows_in(t: torch.Tensor) -> torch.Tensor:
+    """An input operand the kernels can read: last dim contiguous, 16-byte aligned rows."""
+    return t if _aligned(t) else t.contiguous()
+
+
+def _rows_out(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not _aligned(t):
+        raise ValueError(f"{name}: output rows must be contiguous in the last dim and 16-byte aligned")
+    return t
+
+
+def _f32(t: Optional[torch.Tensor], device) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or t.device != device or not t.is_contiguous():
+        t = t.to(device=device, dtype=torch.float32).contiguous()
+    return t
+
+
+def _i32(t: Optional[torch.Tensor], device) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or t.device != device or not t.is_contiguous():
+        t = t.to(device=device, dtype=torch.int32).contiguous()
+    return t
+
+
+def _tables(cos, sin, device):
+    if cos is None:
+        return None, None, 0
+    c, s = _f32(cos, device), _f32(sin, device)
+    if c.dim() != 2 or c.shape != s.shape:
+        raise ValueError("cos/sin tables must both be (max_pos, head_dim/2)")
+    return c, s, c.shape[0]
+
+
+# ---------------------------------------------------------------------------
+# QK-Norm + RoPE + cache placement
+# ---------------------------------------------------------------------------
+
+def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = None,
+                 v: Optional[torch.Tensor] = None, *,
+                 q_out: Optional[torch.Tensor] = None, k_out: Optional[torch.Tensor] = None,
+                 v_out: Optional[torch.Tensor] = None,
+                 q_weight: Optional[torch.Tensor] = None, k_weight: Optional[torch.Tensor] = None,
+                 eps: float = 1e-6, cos: torch.Tensor, sin: torch.Tensor,
+                 position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
+                 pos_base: Optional[torch.Tensor] = None,
+                 kv_row_offset: int = 0, kv_row_base: Optional[torch.Tensor] = None):
+    """QK-Norm + rotate-half RoPE of Q/K rows and a row copy of V, in one launch.
+
+    q: (B, Hq, S, D), k/v: (B, Hkv, S, D), any (b, h, s) strides.  Outputs
+    default to fresh (B, H, S, D) tensors; K/V rows land at row
+    ``kv_row_offset + s`` (or ``kv_row_base[b] + s``) of k_out/v_out, which may
+    be a preallocated cache (B, Hkv, T_cap, D) -- the append of
+    KVCache.update (model/attention.py:31-38).  Positions are
+    ``position_ids[b, s]``, else ``pos_base[b] + s``, else ``pos_offset + s``
+    (model/rope.py:123-129).  Norm weights None skip the norm.
+    Returns (q_out, k_out, v_out).
+    """
+    ref = next(t for t in (q, k, v) if t is not None)
+    _require_device(q, k, v, q_out, k_out, v_out)
+    dev = ref.device
+    B, _, S, D = ref.shape
+    Hq = q.shape[1] if q is not None else 0
+    Hkv = (k if k is not None else v).shape[1] if (k is not None or v is not None) else 0
+    dt_in = _code(ref)
+    for t in (q, k, v):
+        if t is not None and t.dtype != ref.dtype:
+            raise TypeError("q, k and v must share one dtype")
+    q = _rows_in(q) if q is not None else None
+    k = _rows_in(k) if k is not None else None
+    v = _rows_in(v) if v is not None else None
+    if q is not None and q_out is None:
+        q_out = torch.empty(B, Hq, S, D, dtype=ref.dtype, device=dev)
+    if k is not None and k_out is None:
+        k_out = torch.empty(B, Hkv, S, D, dtype=ref.dtype, device=dev)
+    if v is not None and v_out is None:
+        v_out = torch.empty(B, Hkv, S, D, dtype=ref.dtype, device=dev)
+    outs = [t for t in (q_out, k_out, v_out) if t is not None]
+    dt_out = _code(outs[0])
+    for t in outs:
+        if t.dtype != outs[0].dtype:
+            raise TypeError("outputs must share one dtype")
+    for name, t in (("q_out", q_out), ("k_out", k_out), ("v_out", v_out)):
+        if t is not None:
+            _rows_out(t, name)
+    for name, src, dst in (("k", k, k_out), ("v", v, v_out)):
+        if src is not None and kv_row_base is None and kv_row_offset + S > dst.shape[2]:
+            raise ValueError(f"{name}_out has {dst.shape[2]} rows; rows up to {kv_row_offset + S} needed")
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    pos = _i32(position_ids, dev)
+    if pos is not None and tuple(pos.shape) != (B, S):
+        pos = pos.expand(B, S).contiguous()
+    pb = _i32(pos_base, dev)
+    rb = _i32(kv_row_base, dev)
+    qw, kw = _f32(q_weight, dev), _f32(k_weight, dev)
+    lib = _lib.load()
+    st = _lib.strides3
+    rc = lib.nq_qk_norm_rope(
+        _ptr(q), st(q.stride()[:3]) if q is not None else None,
+        _ptr(q_out), st(q_out.stride()[:3]) if q is not None else None,
+        _ptr(k), st(k.stride()[:3]) if k is not None else None,
+        _ptr(k_out), st(k_out.stride()[:3]) if k is not None else None,
+        _ptr(v), st(v.stride()[:3]) if v is not None else None,
+        _ptr(v_out), st(v_out.stride()[:3]) if v is not None else None,
+        B, S, max(Hq, 1), max(Hkv, 1), D, dt_in, dt_out,
+        _ptr(qw), _ptr(kw), float(eps),
+        _ptr(cos_t), _ptr(sin_t), max_pos,
+        _ptr(pos), _ptr(pb), int(pos_offset), _ptr(rb), int(kv_row_offset), _stream(ref))
+    _lib.check(rc, "nq_qk_norm_rope")
+    return q_out, k_out, v_out
+
+
+# ---------------------------------------------------------------------------
+# Prefill
+# ---------------------------------------------------------------------------
+
+def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                      q_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                      cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                      position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
+                      pos_base: Optional[torch.Tensor] = None,
+                      causal: bool = True, sm_scale: Optional[float] = None,
+                      out: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """GQA prefill attention with QK-Norm + RoPE of Q fused into its load.
+
+    q: (B, Hq, S, D) pre-norm queries (norm/rope skipped when q_weight / cos
+    are None); k: (B, Hkv, T, D) keys as stored (already normed and rotated);
+    v: (B, Hkv, T, D).  ``causal`` keeps key j for query i iff j <= i + T - S.
+    Returns o shaped (B, Hq, S, D); by default it is a transposed view of a
+    contiguous (B, S, Hq, D) buffer, so ``o.transpose(1, 2).reshape(B, S, -1)``
+    (o_proj's input, model/attention.py:117) costs nothing.  With
+    ``return_lse`` also returns the fp32 (B, Hq, S) log-sum-exp.
+    """
+    _require_device(q, k, v, out)
+    B, Hq, S, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise TypeError("q, k and v must share one dtype")
+    dt = _code(q)
+    q, k, v = _rows_in(q), _rows_in(k), _rows_in(v)
+    if out is None:
+        out = torch.empty(B, S, Hq, D, dtype=q.dtype, device=q.device).transpose(1, 2)
+    elif tuple(out.shape) != (B, Hq, S, D) or out.dtype != q.dtype:
+        raise ValueError(f"out must be (B, Hq, S, D) = {(B, Hq, S, D)} in {q.dtype}")
+    _rows_out(out, "out")
+    lse = torch.empty(B, Hq, S, dtype=torch.float32, device=q.device) if return_lse else None
+    dev = q.device
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    pos = _i32(position_ids, dev)
+    if pos is not None and tuple(pos.shape) != (B, S):
+        pos = pos.expand(B, S).contiguous()
+    pb = _i32(pos_base, dev)
+    qw = _f32(q_weight, dev)
+    st = _lib.strides3
+    rc = _lib.load().nq_attn_prefill_fwd(
+        _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
+        _ptr(out), st(out.stride()[:3]), _ptr(lse),
+        B, Hq, Hkv, S, T, D, dt, _ptr(qw), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
+        _ptr(pos), _ptr(pb), int(pos_offset), int(bool(causal)),
+        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    _lib.check(rc, "nq_attn_prefill_fwd")
+    return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------
+# Decode
+# ---------------------------------------------------------------------------
+
+def decode_workspace_bytes(B: int, Hq: int, D: int, max_len: int, chunk: int = 0) -> int:
+    """Workspace size attention_decode needs for these sizes."""
+    return int(_lib.load().nq_attn_decode_workspace_bytes(B, Hq, D, max_len, chunk))
+
+
+def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     lens: Optional[torch.Tensor] = None, *, max_len: int,
+                     q_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                     cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                     q_pos: Optional[torch.Tensor] = None, q_pos0: int = -1,
+                     sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None, chunk: int = 0) -> torch.Tensor:
+    """Single-token GQA decode against a ragged (B, Hkv, T_cap, D) cache.
+
+    q: (B, Hq, D) or (B, Hq, 1, D) pre-norm query; keys [0, lens[b]) of the
+    cache are attended (all ``max_len`` rows when lens is None).  The query
+    is rotated at q_pos[b], else q_pos0, else lens[b] - 1 (q_pos0 < 0).
+    Returns (B, Hq, D).
+    """
+    _require_device(q, k_cache, v_cache, lens, out)
+    if q.dim() == 4:
+        q = q[:, :, 0]
+    B, Hq, D = q.shape
+    Hkv, Tcap = k_cache.shape[1], k_cache.shape[2]
+    if k_cache.shape != v_cache.shape or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise ValueError("cache shapes do not match q")
+    if not 0 < max_len <= Tcap:
+        raise ValueError(f"max_len must be in [1, T_cap={Tcap}], got {max_len}")
+    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
+        raise TypeError("q and the caches must share one dtype")
+    dt = _code(q)
+    q = _rows_in(q)
+    _rows_out(k_cache, "k_cache")
+    _rows_out(v_cache, "v_cache")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
+    dev = q.device
+    need = decode_workspace_bytes(B, Hq, D, max_len, chunk)
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    lens_t = _i32(lens, dev)
+    qp = _i32(q_pos, dev)
+    qw = _f32(q_weight, dev)
+    q_str = (ctypes.c_int64 * 2)(q.stride(0), q.stride(1))
+    o_str = (ctypes.c_int64 * 2)(out.stride(0), out.stride(1))
+    st = _lib.strides3
+    rc = _lib.load().nq_attn_decode_fwd(
+        _ptr(q), q_str, _ptr(k_cache), st(k_cache.stride()[:3]), _ptr(v_cache),
+        st(v_cache.stride()[:3]), _ptr(lens_t), _ptr(out), o_str, _ptr(workspace), wbytes,
+        B, Hq, Hkv, D, int(max_len), int(chunk), dt, _ptr(qw), float(eps),
+        _ptr(cos_t), _ptr(sin_t), max_pos, _ptr(qp), int(q_pos0),
+        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    _lib.check(rc, "nq_attn_decode_fwd")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Mirrors of the reference kernel API
+# ---------------------------------------------------------------------------
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
+                    sm_scale: Optional[float] = None) -> torch.Tensor:
+    """kernels/flash_attn.py:130-143 on the gfx950 prefill kernel.
+
+    q: (B, H, N, D), k/v: (B, Hkv, N, D) with H % Hkv == 0 (the reference
+    requires Hkv == H; GQA is accepted here).  Like the reference, inputs that
+    require grad take torch's SDPA instead (flash_attn.py:139).  Returns a
+    contiguous (B, H, N, D) tensor.
+    """
+    _require_device(q, k, v)
+    if q.requires_grad or k.requires_grad or v.requires_grad:
+        G = q.shape[1] // k.shape[1]
+        kk = k.repeat_interleave(G, 1) if G > 1 else k
+        vv = v.repeat_interleave(G, 1) if G > 1 else v
+        return torch.nn.functional.scaled_dot_product_attention(q, kk, vv, is_causal=causal,
+                                                                scale=sm_scale)
+    B, H, N, D = q.shape
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    return attention_prefill(q, k, v, causal=causal, sm_scale=sm_scale, out=out)
+
+
+def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
+               sin: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """kernels/rope.py:99-108: rotate-half RoPE of q and k, in place.
+
+    q: (B, Hq, S, D), k: (B, Hk, S, D); cos/sin: (S, D/2) rows for positions
+    0..S-1, or (B, S, D/2) per-batch rows.  Arithmetic is fp32.
+    """
+    _require_device(q, k)
+    B, _, S, D = q.shape
+    if cos.dim() == 3:
+        tab_c, tab_s = cos.reshape(B * S, D // 2), sin.reshape(B * S, D // 2)
+        pos_base = torch.arange(B, device=q.device, dtype=torch.int32) * S
+    else:
+        tab_c, tab_s, pos_base = cos, sin, None
+    qq, kk = _rows_in(q), _rows_in(k)
+    qk_norm_rope(q=qq, k=kk, q_out=qq, k_out=kk, cos=tab_c, sin=tab_s, pos_base=pos_base)
+    if qq is not q:
+        q.copy_(qq)
+    if kk is not k:
+        k.copy_(kk)
+    return q, k

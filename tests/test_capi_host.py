@@ -1,0 +1,122 @@
+"""CPU-side checks of the boundary: C-ABI exports, host logic, no-CPU-path guarantees."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import nano_qwen_amd as nq
+from nano_qwen_amd import _lib
+from nano_qwen_amd.config import AttentionConfig
+from tests.conftest import ROOT
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "nq_attn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert _header_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libnqattn.so is not built (run python -m nano_qwen_amd.build)")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+    loaded = _lib.load()
+    assert loaded.nq_version() == 100
+    assert loaded.nq_last_error() == b""
+
+
+def test_argument_errors_need_no_gpu():
+    """Validation happens before any HIP call, so it is testable on the CPU."""
+    lib = _lib.load()
+    st = _lib.strides3((0, 0, 0))
+    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None,
+                                 1, 8, 2, 4, 4, 96, 0, None, 1e-6, None, None, 0,
+                                 None, None, 0, 1, 0.0, None)
+    assert rc == _lib.NQ_ERR_UNSUPPORTED and b"head_dim" in lib.nq_last_error()
+    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None,
+                                 1, 8, 3, 4, 4, 128, 0, None, 1e-6, None, None, 0,
+                                 None, None, 0, 1, 0.0, None)
+    assert rc == _lib.NQ_ERR_INVALID and b"divisible" in lib.nq_last_error()
+    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None,
+                                 1, 8, 2, 8, 4, 128, 0, None, 1e-6, None, None, 0,
+                                 None, None, 0, 1, 0.0, None)
+    assert rc == _lib.NQ_ERR_INVALID and b"S <= T" in lib.nq_last_error()
+    assert lib.nq_attn_decode_workspace_bytes(64, 64, 128, 32768, 1024) == 64 * 64 * 32 * 130 * 4
+    assert lib.nq_attn_decode_workspace_bytes(2, 8, 128, 1000, 1024) == 0
+    rc = lib.nq_attn_decode_fwd(None, None, None, st, None, st, None, None, None, None, 0,
+                                2, 8, 2, 128, 5000, 1024, 0, None, 1e-6, None, None, 0,
+                                None, -1, 0.0, None)
+    assert rc == _lib.NQ_ERR_INVALID
+
+
+def test_cpu_tensors_are_refused():
+    q = torch.zeros(1, 2, 4, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        nq.attention_prefill(q, q[:, :1], q[:, :1])
+    cfg = AttentionConfig(hidden_size=128, num_attention_heads=2, num_key_value_heads=1,
+                          head_dim=64, max_position_embeddings=64)
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        nq.Attention(cfg)(torch.zeros(1, 3, 128))
+
+
+def test_state_dict_keys_match_reference_layout():
+    cfg = AttentionConfig(hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
+                          max_position_embeddings=128)
+    attn = nq.Attention(cfg)
+    assert sorted(attn.state_dict()) == sorted([
+        "q_proj.weight", "k_proj.weight", "v_proj.weight", "o_proj.weight",
+        "q_norm.weight", "k_norm.weight"])
+    assert attn.q_proj.weight.shape == (8 * 32, 256)
+    assert attn.k_proj.weight.shape == (2 * 32, 256)
+    assert attn.num_kv_groups == 4 and attn.head_dim == 32
+
+
+def test_config_from_yaml_keeps_attention_fields(tmp_path):
+    p = tmp_path / "m.yaml"
+    p.write_text("hidden_size: 4096\nnum_hidden_layers: 94\nnum_attention_heads: 64\n"
+                 "num_key_value_heads: 4\nhead_dim: 128\nmax_position_embeddings: 131072\n"
+                 "rope_theta: 1000000.0\nnum_experts: 128\n")
+    cfg = AttentionConfig.from_yaml(p)
+    assert (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim) == (64, 4, 128)
+    assert cfg.num_kv_groups == 16 and cfg.rope_theta == 1e6
+    assert AttentionConfig(hidden_size=2048, num_attention_heads=16).head_dim == 128
+
+
+def test_rope_tables_match_reference_rows():
+    import numpy as np
+    from tests.conftest import GOLDEN
+    fr = np.load(os.path.join(GOLDEN, "rope_tables.npz"), allow_pickle=False)
+    rows = torch.from_numpy(fr["rows"])
+    rope = nq.RotaryEmbedding(128, 131072, 1e6, {"type": "yarn", "factor": 4.0,
+                                                 "original_max_position_embeddings": 32768})
+    np.testing.assert_array_equal(rope.cos_cached[rows].numpy(), fr["yarn128_cos"])
+    np.testing.assert_array_equal(rope.sin_cached[rows].numpy(), fr["yarn128_sin"])
+    cos, sin = nq.build_tables(128, 131072, 1e6)
+    np.testing.assert_array_equal(cos[rows].numpy(), fr["plain128_cos"])
+    np.testing.assert_array_equal(sin[rows].numpy(), fr["plain128_sin"])
+
+
+def test_kvcache_host_semantics_match_concatenation():
+    """update() on host tensors behaves like the reference's torch.cat cache."""
+    g = torch.Generator().manual_seed(0)
+    cache = nq.KVCache()
+    ks, vs = [], []
+    for S in (5, 1, 1, 70, 1):
+        k = torch.randn(2, 3, S, 64, generator=g)
+        v = torch.randn(2, 3, S, 64, generator=g)
+        ks.append(k), vs.append(v)
+        K, V = cache.update(k, v)
+        torch.testing.assert_close(K, torch.cat(ks, 2), rtol=0, atol=0)
+        torch.testing.assert_close(V, torch.cat(vs, 2), rtol=0, atol=0)
+    assert cache.seq_len == 78 and cache.capacity >= 78
+    cache.reset()
+    assert cache.seq_len == 0 and cache.key.shape[2] == 0

@@ -1,0 +1,190 @@
+"""GPU parity of the prefill attention kernel against the oracle (fp32 reference math)."""
+
+import math
+
+import pytest
+import torch
+
+import nano_qwen_amd as nq
+from oracle import attention, attention_path, rms_norm, rope_tables, rotate_half
+from tests.helpers import BF16_MAX_ABS, BF16_MEAN_ABS, assert_bf16_close, err_stats, randn, say
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def gpu_attention(q, k, v, qw, kw, eps, cos, sin, causal=True, position_ids=None, pos_offset=0):
+    """The drop-in's prefill sequence: K-Norm+RoPE row kernel, then the fused prefill kernel."""
+    kh = nq.qk_norm_rope(k=k, k_weight=kw, eps=eps, cos=cos, sin=sin, position_ids=position_ids,
+                         pos_offset=pos_offset)[1]
+    return nq.attention_prefill(q, kh, v, q_weight=qw, eps=eps, cos=cos, sin=sin,
+                                position_ids=position_ids, pos_offset=pos_offset, causal=causal)
+
+
+def make(B, S, Hq, Hkv, D, dtype, seed, model_layout=True, wscale=0.02):
+    if model_layout:  # (B, S, H, D) storage viewed as (B, H, S, D), as q_proj(...).view().transpose()
+        q = randn(B, S, Hq, D, seed=seed, dtype=dtype).transpose(1, 2)
+        k = randn(B, S, Hkv, D, seed=seed + 1, dtype=dtype).transpose(1, 2)
+        v = randn(B, S, Hkv, D, seed=seed + 2, dtype=dtype).transpose(1, 2)
+    else:
+        q = randn(B, Hq, S, D, seed=seed, dtype=dtype)
+        k = randn(B, Hkv, S, D, seed=seed + 1, dtype=dtype)
+        v = randn(B, Hkv, S, D, seed=seed + 2, dtype=dtype)
+    qw = 1 + wscale * randn(D, seed=seed + 3)
+    kw = 1 + wscale * randn(D, seed=seed + 4)
+    return q, k, v, qw, kw
+
+
+def run_case(B, S, Hq, Hkv, D, dtype, seed, causal=True, rope_scaling=None, max_pos=None,
+             pos_offset=0, model_layout=True):
+    q, k, v, qw, kw = make(B, S, Hq, Hkv, D, dtype, seed, model_layout)
+    max_pos = max_pos or (S + pos_offset)
+    cos, sin = rope_tables(D, max_pos, 1e6, rope_scaling)
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV), causal=causal, pos_offset=pos_offset)
+    torch.cuda.synchronize()
+    pos = torch.arange(pos_offset, pos_offset + S)
+    ref = attention_path(q.float(), k.float(), v.float(), q_weight=qw, k_weight=kw, eps=1e-6,
+                         cos=cos, sin=sin, q_pos=pos, causal=causal)
+    return o.cpu(), ref
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_debug_scale_config(dtype):
+    """B2 S256 Hq8 Hkv2 D64 causal, norm weights 1, theta 1e6 (the CPU-runnable config)."""
+    say(f"prefill debug config {dtype}")
+    q, k, v, _, _ = make(2, 256, 8, 2, 64, dtype, seed=1000)
+    ones = torch.ones(64)
+    cos, sin = rope_tables(64, 256, 1e6)
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), ones.to(DEV), ones.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV))
+    ref = attention_path(q.float(), k.float(), v.float(), q_weight=ones, k_weight=ones, eps=1e-6,
+                         cos=cos, sin=sin, q_pos=torch.arange(256), causal=True)
+    assert o.dtype == dtype
+    assert_bf16_close(o, ref, "debug config")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (16, 8), (32, 8), (32, 4), (32, 2)])
+@pytest.mark.parametrize("S", [1, 77, 300])
+def test_gqa_group_sizes(Hq, Hkv, S):
+    say(f"prefill G={Hq // Hkv} S={S}")
+    o, ref = run_case(2, S, Hq, Hkv, 128, torch.bfloat16, seed=7 + S)
+    assert_bf16_close(o, ref, f"G={Hq // Hkv} S={S}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_non_causal(D):
+    say(f"prefill non-causal D={D}")
+    o, ref = run_case(2, 150, 8, 2, D, torch.bfloat16, seed=21, causal=False)
+    assert_bf16_close(o, ref, "non-causal")
+
+
+def test_contiguous_bhsd_inputs():
+    say("prefill BHSD inputs")
+    o, ref = run_case(1, 200, 16, 8, 128, torch.bfloat16, seed=23, model_layout=False)
+    assert_bf16_close(o, ref, "bhsd")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_queries_after_cached_keys(causal):
+    """S < T: queries are the last S of T positions (causal is bottom-right aligned)."""
+    say(f"prefill S<T causal={causal}")
+    B, S, T, Hq, Hkv, D = 2, 45, 203, 8, 2, 128
+    q = randn(B, Hq, S, D, seed=31, dtype=torch.bfloat16)
+    k = randn(B, Hkv, T, D, seed=32, dtype=torch.bfloat16)
+    v = randn(B, Hkv, T, D, seed=33, dtype=torch.bfloat16)
+    o = nq.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
+    ref = attention(q.float(), k.float(), v.float(), causal=causal, causal_offset=T - S)
+    assert_bf16_close(o, ref, "S<T")
+
+
+def test_flash_attention_mirror_and_lse():
+    say("flash_attention mirror + lse")
+    B, H, N, D = 2, 4, 190, 64
+    q = randn(B, H, N, D, seed=41, dtype=torch.bfloat16)
+    k = randn(B, H, N, D, seed=42, dtype=torch.bfloat16)
+    v = randn(B, H, N, D, seed=43, dtype=torch.bfloat16)
+    o = nq.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    assert o.shape == (B, H, N, D) and o.is_contiguous()
+    assert_bf16_close(o, attention(q.float(), k.float(), v.float(), causal=True), "flash")
+    scale = 0.3
+    o2, lse = nq.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, sm_scale=scale,
+                                   return_lse=True)
+    assert_bf16_close(o2, attention(q.float(), k.float(), v.float(), causal=True, scale=scale), "scale")
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2)) * scale
+    s = s.masked_fill(torch.ones(N, N, dtype=torch.bool).triu(1), float("-inf"))
+    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-3, atol=2e-2)
+
+
+def test_explicit_position_ids_and_yarn_high_positions():
+    say("prefill position_ids + YaRN")
+    B, S, Hq, Hkv, D = 2, 96, 8, 2, 128
+    yarn = {"type": "yarn", "factor": 4.0, "original_max_position_embeddings": 32768}
+    q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=51)
+    cos, sin = rope_tables(D, 131072, 1e6, yarn)
+    pos = torch.stack([torch.arange(S) + 131072 - S - 7 * b for b in range(B)])
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV), position_ids=pos.to(DEV))
+    ref = attention_path(q.float(), k.float(), v.float(), q_weight=qw, k_weight=kw, eps=1e-6,
+                         cos=cos, sin=sin, q_pos=pos, causal=True)
+    assert_bf16_close(o, ref, "yarn positions")
+
+
+def test_qwen3_1p7b_like_full_size():
+    """B8 S2048 Hq16 Hkv8 D128 bf16; oracle on batches 0 and 7 (all heads, all rows)."""
+    say("prefill Qwen3-1.7B-like B8 S2048")
+    B, S, Hq, Hkv, D = 8, 2048, 16, 8, 128
+    q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=1001)
+    cos, sin = rope_tables(D, S, 1e6)
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV)).cpu()
+    assert torch.isfinite(o.float()).all()
+    for b in (0, 7):
+        ref = attention_path(q[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(),
+                             q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin,
+                             q_pos=torch.arange(S), causal=True)
+        assert_bf16_close(o[b:b + 1], ref, f"1.7B b={b}")
+
+
+def _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows):
+    """Oracle rows [r0, r1) for batch b, the G heads of kv head kvh (causal from 0)."""
+    kh = rotate_half(rms_norm(k[b:b + 1, kvh:kvh + 1].float(), kw, 1e-6),
+                     cos[None, None], sin[None, None])
+    outs = []
+    for r0, r1 in rows:
+        qs = q[b:b + 1, kvh * G:(kvh + 1) * G, r0:r1].float()
+        qh = rotate_half(rms_norm(qs, qw, 1e-6), cos[r0:r1][None, None], sin[r0:r1][None, None])
+        outs.append(attention(qh, kh[:, :, :r1], v[b:b + 1, kvh:kvh + 1, :r1].float(),
+                              causal=True, causal_offset=r0))
+    return outs
+
+
+def test_qwen3_8b_like_full_size():
+    """B4 S8192 Hq32 Hkv8 D128 bf16; oracle on sampled 128-row blocks."""
+    say("prefill Qwen3-8B-like B4 S8192")
+    B, S, Hq, Hkv, D = 4, 8192, 32, 8, 128
+    G = Hq // Hkv
+    q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=1002)
+    cos, sin = rope_tables(D, S, 1e6)
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV)).cpu()
+    rows = [(0, 128), (4000, 4128), (S - 128, S)]
+    for b, kvh in ((0, 0), (3, 7)):
+        for (r0, r1), ref in zip(rows, _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows)):
+            assert_bf16_close(o[b:b + 1, kvh * G:(kvh + 1) * G, r0:r1], ref, f"8B b={b} kvh={kvh} rows={r0}")
+
+
+def test_long_context_yarn_full_size():
+    """B1 S131072 Hq32 Hkv4 D128 bf16 YaRN x4; oracle on sampled 64-row blocks."""
+    say("prefill YaRN B1 S131072")
+    B, S, Hq, Hkv, D = 1, 131072, 32, 4, 128
+    G = Hq // Hkv
+    yarn = {"type": "yarn", "factor": 4.0, "original_max_position_embeddings": 32768}
+    q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=1004)
+    cos, sin = rope_tables(D, S, 1e6, yarn)
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV)).cpu()
+    rows = [(0, 64), (70000, 70064), (S - 64, S)]
+    for kvh in (0, 3):
+        for (r0, r1), ref in zip(rows, _sampled_blocks(q, k, v, qw, kw, cos, sin, 0, kvh, G, rows)):
+            assert_bf16_close(o[:, kvh * G:(kvh + 1) * G, r0:r1], ref, f"yarn kvh={kvh} rows={r0}")
