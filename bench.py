@@ -207,11 +207,23 @@ def main():
     ap.add_argument("--workloads", default="c2,c3,c4,c5",
                     help="comma list of c2 (headline), c3, c4, c5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (3 times), for scaling "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the attention hot path is built and measured on a "
               "single MI355X (no collectives); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n * 4, "reps": 3}), flush=True)
+        return
     import nano_qwen_amd as nq
     dev = "cuda"
     props = torch.cuda.get_device_properties(0)

@@ -61,6 +61,33 @@ template <> struct Vec8<float> {
 
 __device__ __forceinline__ bf16x8 to_bf16x8(floatx8 v) { return __builtin_convertvector(v, bf16x8); }
 
+// ---------------------------------------------------------------- LDS
+// gfx950 LDS: 64 banks x 4 bytes (256 B per clock).  A ds_read_b128 serves 16
+// lanes per clock, a ds_read_b64 (and the transpose read) 32 lanes per clock.
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16.  Within each group of 16 lanes, source lane j supplies
+// the address of 4 consecutive 16-bit values M[j][0..3]; destination lane i
+// receives (M[i/4][i%4], M[4+i/4][i%4], M[8+i/4][i%4], M[12+i/4][i%4]).
+// Pointing source lane j at row r0 + j/4, column c0 + 4*(j%4) of a row-major
+// tile hands destination lane i the column c0 + i of rows r0 .. r0+3.
+__device__ __forceinline__ shortx4 lds_read_tr4(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) shortx4*)(const_cast<bf16*>(p)));
+}
+
+// Two transpose reads (rows r0..r0+3 and r0+4..r0+7 of one column) as one
+// 8-element MFMA operand.
+__device__ __forceinline__ bf16x8 lds_read_tr8(const bf16* p_lo, const bf16* p_hi) {
+  shortx4 a = lds_read_tr4(p_lo);
+  shortx4 b = lds_read_tr4(p_hi);
+  typedef short shortx8 __attribute__((ext_vector_type(8)));
+  shortx8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, ab);
+}
+
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
 template <typename T>
 __device__ __forceinline__ void store8(T* p, floatx8 v);
 template <>

@@ -58,9 +58,10 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(DC_THREADS, DC_THREAD
 decode_split_kernel(DecodeParams p) {
   constexpr int NDQ = D / 32;         // 32-wide d blocks (QK^T k-steps)
   constexpr int NDO = D / 16;         // 16-wide d blocks (output tiles)
-  constexpr int VS = DC_STEP + 8;     // V^T row stride (elements) in LDS
-  constexpr int V_CH = D / 64;        // 16-byte chunks per lane per key
-  constexpr int WAVE_LDS = D * VS;    // bf16 elements per wave
+  constexpr int CPR = D / 8;          // 16-byte chunks per V row
+  constexpr int VS = D + 16;          // V row stride (elements) in LDS: +32 B
+  constexpr int V_LOADS = DC_STEP * CPR / 64;  // 16-byte V loads per lane per step
+  constexpr int WAVE_LDS = DC_STEP * VS;       // bf16 elements per wave
   constexpr int COMB_F = 4 * 16 * D + 2 * 4 * 16;  // floats for the wave merge
   constexpr int LDS_BYTES = (4 * WAVE_LDS * 2 > COMB_F * 4) ? 4 * WAVE_LDS * 2 : COMB_F * 4;
   __shared__ __attribute__((aligned(16))) unsigned char smem_raw[LDS_BYTES];
@@ -138,8 +139,13 @@ decode_split_kernel(DecodeParams p) {
 
   const T* kbase = reinterpret_cast<const T*>(p.kc) + b * p.ksb + kvh * p.ksh;
   const T* vbase = reinterpret_cast<const T*>(p.vc) + b * p.vsb + kvh * p.vsh;
-  bf16* Vt = reinterpret_cast<bf16*>(smem_raw) + wave * WAVE_LDS;
+  bf16* Vs = reinterpret_cast<bf16*>(smem_raw) + wave * WAVE_LDS;
   const bf16x8 zero8 = {};
+  // V^T operand via transpose reads: lane group grp, j = lane%16: source row
+  // 4*grp + j/4 (+16 for the second half), column 4*(j%4) (+dd*16).  Rows
+  // 16*half + 4*grp + [0,4) are exactly the keys of this lane's P values.
+  const int jj = lane & 15;
+  const int v_off = (4 * grp + (jj >> 2)) * VS + 4 * (jj & 3);
 
   float m_i = -INFINITY, l_i = 0.f;
   floatx4 oacc[NDO];
@@ -149,26 +155,23 @@ decode_split_kernel(DecodeParams p) {
   const int nsteps = (s1 - s0 + DC_STEP - 1) / DC_STEP;
   for (int t = wave; t < nsteps; t += 4) {
     const int k0 = s0 + t * DC_STEP;
-    // K as MFMA A operand: block kb, row r holds key (r/4)*8 + kb*4 + r%4,
-    // so that this lane's P values cover 8 consecutive keys grp*8 + [0, 8).
+    // K as MFMA A operand: block kb, row r holds key kb*16 + r
     bf16x8 ka[2][NDQ];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const int key = k0 + (c16 >> 2) * 8 + kb * 4 + (c16 & 3);
+      const int key = k0 + kb * 16 + c16;
       const bool ok = key < s1;
 #pragma unroll
       for (int dq = 0; dq < NDQ; ++dq)
         ka[kb][dq] = ok ? Vec8<T>::load_bf16(kbase + (int64_t)key * p.kst + dq * 32 + grp * 8) : zero8;
     }
-    // V rows: lane holds keys (lane/8)*4 + [0,4) x chunks (lane%8) + 8*cc
-    bf16x8 vr[4][V_CH];
+    // V rows, whole rows per 16 lanes: chunk c = lane + 64*i
+    bf16x8 vr[V_LOADS];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int key = k0 + (lane >> 3) * 4 + e;
-      const bool ok = key < s1;
-#pragma unroll
-      for (int cc = 0; cc < V_CH; ++cc)
-        vr[e][cc] = ok ? Vec8<T>::load_bf16(vbase + (int64_t)key * p.vst + ((lane & 7) + 8 * cc) * 8) : zero8;
+    for (int i = 0; i < V_LOADS; ++i) {
+      const int c = lane + 64 * i;
+      const int key = k0 + c / CPR;
+      vr[i] = key < s1 ? Vec8<T>::load_bf16(vbase + (int64_t)key * p.vst + (c % CPR) * 8) : zero8;
     }
 
     floatx4 sc[2];
@@ -183,7 +186,7 @@ decode_split_kernel(DecodeParams p) {
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (k0 + grp * 8 + kb * 4 + i >= s1) sc[kb][i] = -INFINITY;
+          if (k0 + kb * 16 + grp * 4 + i >= s1) sc[kb][i] = -INFINITY;
     }
 
     float mx = -INFINITY;
@@ -212,19 +215,17 @@ decode_split_kernel(DecodeParams p) {
 #pragma unroll
     for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
 
-    // V^T into this wave's LDS slab: Vt[d][key], 4 keys per 8-byte write
+    // V rows into this wave's LDS slab (row-major), read back transposed
 #pragma unroll
-    for (int cc = 0; cc < V_CH; ++cc)
-#pragma unroll
-      for (int e8 = 0; e8 < 8; ++e8) {
-        const int d = ((lane & 7) + 8 * cc) * 8 + e8;
-        bf16x4 t4 = {vr[0][cc][e8], vr[1][cc][e8], vr[2][cc][e8], vr[3][cc][e8]};
-        *reinterpret_cast<bf16x4*>(Vt + d * VS + (lane >> 3) * 4) = t4;
-      }
+    for (int i = 0; i < V_LOADS; ++i) {
+      const int c = lane + 64 * i;
+      *reinterpret_cast<bf16x8*>(Vs + (c / CPR) * VS + (c % CPR) * 8) = vr[i];
+    }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int dd = 0; dd < NDO; ++dd) {
-      bf16x8 a = *reinterpret_cast<const bf16x8*>(Vt + (dd * 16 + c16) * VS + grp * 8);
+      const bf16* src = Vs + v_off + dd * 16;
+      bf16x8 a = lds_read_tr8(src, src + 16 * VS);
       oacc[dd] = mfma16(a, pop, oacc[dd]);
     }
     __builtin_amdgcn_wave_barrier();

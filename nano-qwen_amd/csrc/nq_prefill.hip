@@ -16,12 +16,22 @@
 // v_mfma_f32_32x32x16_bf16 (A = K tile from LDS, B = Q from registers).  In
 // the result each lane owns one query column and 16 of its 32 keys, so the
 // row max / row sum of the online softmax need no cross-lane traffic except a
-// single xor-32 exchange.  The output is also kept transposed,
-// O^T += V^T P^T, so the per-row rescale factor applies lane-locally.  The K
-// tile's rows are loaded into MFMA rows through a bit permutation (swap bits 2
-// and 3 of the row index) chosen so that each lane's 8 consecutive P values
-// are 8 consecutive keys; V is stored transposed in LDS (V^T[d][key]) so the
-// PV A-operand is one 16-byte LDS read.
+// single xor-32 exchange.  The output is kept transposed too,
+// O^T += V^T P^T, so the per-row rescale applies lane-locally.  K rows enter
+// MFMA rows through a bit permutation (swap bits 2 and 3 of the row index)
+// chosen so each lane's 8 consecutive P values are 8 consecutive keys; the
+// V^T operand is then read from the row-major V tile with
+// ds_read_b64_tr_b16 (two transpose reads per operand), so V is never
+// transposed on the way into LDS.
+//
+// LDS (64 banks on gfx950): K rows are padded by 16 bytes so the 16 rows one
+// ds_read_b128 touches fall on distinct banks; V rows are padded by 64 bytes
+// so the 4 rows x 64 bytes one transpose read touches do.
+//
+// Softmax: log2 domain (exp2 with log2(e) folded into the scale).  The
+// running max is only raised when some row's tile max exceeds it by more than
+// 2^8 (then O and l are rescaled); otherwise P values up to 256 are
+// accumulated against the stale max.  The final O/l is exact either way.
 //
 // Pipeline: the next K/V tile is fetched from HBM into registers while the
 // current tile's MFMAs run, then written to the other LDS buffer; one barrier
@@ -36,6 +46,7 @@ namespace nq {
 constexpr int PF_THREADS = 256;
 constexpr int PF_ROWS = 128;  // query rows per workgroup
 constexpr int PF_BN = 64;     // keys per tile
+constexpr float PF_RESCALE_LOG2 = 8.0f;
 
 struct PrefillParams {
   const void* q;
@@ -64,22 +75,26 @@ __device__ __forceinline__ int key_perm32(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
+template <int D>
+struct PrefillLds {
+  static constexpr int KS = D + 8;        // K row stride (elements): +16 B
+  static constexpr int VS = D + 32;       // V row stride (elements): +64 B
+  static constexpr int K_TILE = PF_BN * KS;
+  static constexpr int V_TILE = PF_BN * VS;
+  static constexpr int BUF = K_TILE + V_TILE;
+};
+
 template <int D, typename T, bool CAUSAL, bool FUSE_Q>
 __global__ void __attribute__((amdgpu_flat_work_group_size(PF_THREADS, PF_THREADS),
                                amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(PrefillParams p) {
-  constexpr int KS = D + 8;          // K tile row stride (elements), 16 B pad
-  constexpr int VS = PF_BN + 8;      // V^T tile row stride (elements), 16 B pad
-  constexpr int K_TILE = PF_BN * KS;
-  constexpr int V_TILE = D * VS;
-  constexpr int BUF = K_TILE + V_TILE;
+  using Lds = PrefillLds<D>;
+  constexpr int KS = Lds::KS, VS = Lds::VS, K_TILE = Lds::K_TILE, BUF = Lds::BUF;
   constexpr int CPR = D / 8;         // 16-byte chunks per row
   constexpr int NDB = D / 16;        // 16-wide d blocks (QK^T k-steps)
   constexpr int NDO = D / 32;        // 32-wide d blocks (output tiles)
-  constexpr int K_LOADS = PF_BN * CPR / PF_THREADS;
-  constexpr int V_ITEMS = (PF_BN / 4) * CPR;  // (4-key group, chunk) pairs
-  constexpr int V_PER_T = (V_ITEMS + PF_THREADS - 1) / PF_THREADS;
-  static_assert(K_LOADS * PF_THREADS == PF_BN * CPR, "tile must split evenly");
+  constexpr int LOADS = PF_BN * CPR / PF_THREADS;  // per tensor per thread
+  static_assert(LOADS * PF_THREADS == PF_BN * CPR, "tile must split evenly");
 
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * BUF];
 
@@ -152,51 +167,36 @@ prefill_kernel(PrefillParams p) {
   const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.ksb + kvh * p.ksh;
   const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
 
-  bf16x8 kreg[K_LOADS];
-  bf16x8 vreg[V_PER_T][4];
+  // global -> register staging: thread owns 16-byte chunks c = tid + 256*i
+  bf16x8 kreg[LOADS], vreg[LOADS];
   const bf16x8 zero8 = {};
-
   auto load_tile = [&](int n0) {
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
+    for (int i = 0; i < LOADS; ++i) {
       const int c = tid + i * PF_THREADS;
       const int key = n0 + c / CPR, ch = c % CPR;
-      kreg[i] = key < p.T ? Vec8<T>::load_bf16(kbase + (int64_t)key * p.kss + ch * 8) : zero8;
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int item = tid + i * PF_THREADS;
-      const int quad = item / CPR, ch = item % CPR;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = n0 + quad * 4 + e;
-        vreg[i][e] = (item < V_ITEMS && key < p.T)
-                         ? Vec8<T>::load_bf16(vbase + (int64_t)key * p.vss + ch * 8)
-                         : zero8;
-      }
+      const bool ok = key < p.T;
+      kreg[i] = ok ? Vec8<T>::load_bf16(kbase + (int64_t)key * p.kss + ch * 8) : zero8;
+      vreg[i] = ok ? Vec8<T>::load_bf16(vbase + (int64_t)key * p.vss + ch * 8) : zero8;
     }
   };
   auto store_tile = [&](int buf) {
     bf16* Ks = smem + buf * BUF;
-    bf16* Vt = Ks + K_TILE;
+    bf16* Vs = Ks + K_TILE;
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
+    for (int i = 0; i < LOADS; ++i) {
       const int c = tid + i * PF_THREADS;
       *reinterpret_cast<bf16x8*>(Ks + (c / CPR) * KS + (c % CPR) * 8) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int item = tid + i * PF_THREADS;
-      if (item < V_ITEMS) {
-        const int quad = item / CPR, ch = item % CPR;
-#pragma unroll
-        for (int e8 = 0; e8 < 8; ++e8) {
-          bf16x4 t = {vreg[i][0][e8], vreg[i][1][e8], vreg[i][2][e8], vreg[i][3][e8]};
-          *reinterpret_cast<bf16x4*>(Vt + (ch * 8 + e8) * VS + quad * 4) = t;
-        }
-      }
+      *reinterpret_cast<bf16x8*>(Vs + (c / CPR) * VS + (c % CPR) * 8) = vreg[i];
     }
   };
+
+  // per-lane LDS offsets (elements within a buffer)
+  const int k_off = key_perm32(r32) * KS + hh * 8;
+  // V^T operand via transpose reads: lane group gi = lane/16, j = lane%16;
+  // source row hh*8 + j/4 (+ks*16 + 4*half), column (gi&1)*16 + 4*(j%4) (+dd*32)
+  const int gi = lane >> 4, jj = lane & 15;
+  const int v_off = K_TILE + (hh * 8 + (jj >> 2)) * VS + (gi & 1) * 16 + 4 * (jj & 3);
 
   float m_i = -INFINITY, l_i = 0.f;
   floatx16 oacc[NDO];
@@ -207,26 +207,21 @@ prefill_kernel(PrefillParams p) {
   store_tile(0);
   __syncthreads();
 
-  const int krow_perm = key_perm32(r32);
   for (int j = 0; j < ntiles; ++j) {
     const int n0 = j * PF_BN;
     const int buf = j & 1;
     if (j + 1 < ntiles) load_tile(n0 + PF_BN);
-    const bf16* Ks = smem + buf * BUF;
-    const bf16* Vt = Ks + K_TILE;
+    const bf16* Bs = smem + buf * BUF;
 
-    // S^T = K Q^T for two 32-key blocks
-    floatx16 s[2];
+    // S^T = K Q^T for two 32-key blocks (chains interleaved)
+    floatx16 s[2] = {floatx16{}, floatx16{}};
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = floatx16{};
-      const bf16* krow = Ks + (kb * 32 + krow_perm) * KS + hh * 8;
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(krow + db * 16);
+      for (int kb = 0; kb < 2; ++kb) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(Bs + k_off + kb * 32 * KS + db * 16);
         s[kb] = mfma32(a, qop[db], s[kb]);
       }
-    }
 
     // masking: keys past T, and (causal) keys past this row's frontier
     const bool need_mask = (n0 + PF_BN > p.T) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff);
@@ -247,10 +242,16 @@ prefill_kernel(PrefillParams p) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float m_new = fmaxf(m_i, mx * p.scale_log2);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_i - m_use);
+    mx = fmaxf(mx, shfl_xor_f(mx, 32)) * p.scale_log2;
+    if (wave_any(mx > m_i + PF_RESCALE_LOG2)) {
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = fast_exp2(m_i - m_new);  // 0 on the first tile
+      l_i *= alpha;
+#pragma unroll
+      for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
+      m_i = m_new;
+    }
+    // every row has seen key 0 by now, so m_i is finite
     float rs = 0.f;
     bf16x8 pop[4];
 #pragma unroll
@@ -260,27 +261,23 @@ prefill_kernel(PrefillParams p) {
         floatx8 t;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float pe = fast_exp2(s[kb][half * 8 + e] * p.scale_log2 - m_use);
+          const float pe = fast_exp2(s[kb][half * 8 + e] * p.scale_log2 - m_i);
           rs += pe;
           t[e] = pe;
         }
         pop[kb * 2 + half] = to_bf16x8(t);
       }
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-#pragma unroll
-    for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
+    l_i += rs;
 
     // O^T += V^T P^T
 #pragma unroll
-    for (int dd = 0; dd < NDO; ++dd) {
-      const bf16* vrow = Vt + (dd * 32 + r32) * VS + hh * 8;
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(vrow + ks * 16);
+      for (int dd = 0; dd < NDO; ++dd) {
+        const bf16* src = Bs + v_off + ks * 16 * VS + dd * 32;
+        bf16x8 a = lds_read_tr8(src, src + 4 * VS);
         oacc[dd] = mfma32(a, pop[ks], oacc[dd]);
       }
-    }
 
     if (j + 1 < ntiles) store_tile(buf ^ 1);
     __syncthreads();
