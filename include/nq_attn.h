@@ -87,9 +87,11 @@ int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
  * already normalised and rotated by nq_qk_norm_rope, V raw), the GQA
  * expansion of attention.py:106-108 is implicit, and SDPA is replaced.
  *
- * q: (B, Hq, S, D) with strides q_strides; k, v: (B, Hkv, T, D); o: output
- *   (B, Hq, S, D) with strides o_strides (pass the strides of a
- *   (B, S, Hq, D) buffer to get o_proj's input layout directly).
+ * q: (B, Hq, S, D) with strides q_strides; k, v: (B, Hkv, T, D), always
+ *   bf16 (their tiles are copied into LDS unconverted; callers holding fp32
+ *   K/V convert them first); o: output (B, Hq, S, D) with strides o_strides
+ *   (pass the strides of a (B, S, Hq, D) buffer to get o_proj's input layout
+ *   directly).  q and o use `dtype`.
  * lse: optional fp32 (B, Hq, S) natural-log sum-exp of the scaled scores.
  * q_weight: RMSNorm weight for Q (NULL = none); cos_tab/sin_tab: RoPE table
  *   for Q (NULL = none); q_pos / q_pos_base / q_pos0: Q positions as in

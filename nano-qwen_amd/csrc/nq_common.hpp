@@ -88,6 +88,19 @@ __device__ __forceinline__ bf16x8 lds_read_tr8(const bf16* p_lo, const bf16* p_h
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
+// global_load_lds_dwordx4: lane t copies 16 bytes from its global address to
+// LDS at lds + 16*t (lds must be wave-uniform; it is passed through M0).
+// Completion is tracked by vmcnt.  (Kept in a non-template function: naming
+// the builtin directly inside a kernel template made the host pass drop that
+// kernel's launch stubs.)
+__device__ __forceinline__ void global_load_lds16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): all of this wave's vector-memory loads (including
+// global_load_lds) have completed.
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x3f70); }
+
 template <typename T>
 __device__ __forceinline__ void store8(T* p, floatx8 v);
 template <>

@@ -20,23 +20,26 @@
 // O^T += V^T P^T, so the per-row rescale applies lane-locally.  K rows enter
 // MFMA rows through a bit permutation (swap bits 2 and 3 of the row index)
 // chosen so each lane's 8 consecutive P values are 8 consecutive keys; the
-// V^T operand is then read from the row-major V tile with
-// ds_read_b64_tr_b16 (two transpose reads per operand), so V is never
-// transposed on the way into LDS.
+// V^T operand is read from the row-major V tile with ds_read_b64_tr_b16.
 //
-// LDS (64 banks on gfx950): K rows are padded by 16 bytes so the 16 rows one
-// ds_read_b128 touches fall on distinct banks; V rows are padded by 64 bytes
-// so the 4 rows x 64 bytes one transpose read touches do.
+// Memory pipeline: K and V tiles (64 keys) travel HBM -> LDS directly with
+// global_load_lds_dwordx4 (no staging registers, no LDS store instructions).
+// K and V are double-buffered separately and K runs one tile ahead: iteration
+// j issues the loads of K[j+2] and V[j+1], computes S[j+1] = K[j+1] Q^T (its
+// MFMAs overlap the softmax VALU work of tile j) and then O += V[j] P[j].
+// Every load has one full iteration to land; one barrier per tile.
+//
+// LDS (64 banks on gfx950): rows are unpadded and their 16-byte chunks are
+// XOR-swizzled by row, so the 16 rows one ds_read_b128 of K touches, and the
+// 4 rows x 64 bytes one transpose read of V touches, fall on distinct banks.
 //
 // Softmax: log2 domain (exp2 with log2(e) folded into the scale).  The
 // running max is only raised when some row's tile max exceeds it by more than
-// 2^8 (then O and l are rescaled); otherwise P values up to 256 are
-// accumulated against the stale max.  The final O/l is exact either way.
-//
-// Pipeline: the next K/V tile is fetched from HBM into registers while the
-// current tile's MFMAs run, then written to the other LDS buffer; one barrier
-// per 64-key tile.  Causal workgroups are issued heaviest (last q-block)
-// first.
+// 2^8 (then O and l are rescaled); otherwise P values up to 256 accumulate
+// against the stale max.  The final O/l is exact either way.
+// Causal workgroups are issued heaviest (last q-block) first.
+
+#include <type_traits>
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
@@ -76,29 +79,30 @@ __device__ __forceinline__ int key_perm32(int r) {
 }
 
 template <int D>
-struct PrefillLds {
-  static constexpr int KS = D + 8;        // K row stride (elements): +16 B
-  static constexpr int VS = D + 32;       // V row stride (elements): +64 B
-  static constexpr int K_TILE = PF_BN * KS;
-  static constexpr int V_TILE = PF_BN * VS;
-  static constexpr int BUF = K_TILE + V_TILE;
+struct PfTile {
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int CPR = D / 8;                   // 16-byte chunks per row
+  static constexpr int RPL = 256 / ROW_BYTES;         // rows per 256-byte bank line
+  static constexpr int TILE_BYTES = PF_BN * ROW_BYTES;
+  static constexpr int LOADS = TILE_BYTES / 1024 / 4; // 1 KiB load instructions per wave
+  // physical chunk of logical chunk c in row r
+  __device__ static int k_chunk(int r, int c) { return c ^ ((r / RPL) & (CPR - 1)); }
+  __device__ static int v_chunk(int r, int c) { return c ^ (4 * ((r / RPL) & (D / 32 - 1))); }
 };
 
 template <int D, typename T, bool CAUSAL, bool FUSE_Q>
 __global__ void __attribute__((amdgpu_flat_work_group_size(PF_THREADS, PF_THREADS),
                                amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(PrefillParams p) {
-  using Lds = PrefillLds<D>;
-  constexpr int KS = Lds::KS, VS = Lds::VS, K_TILE = Lds::K_TILE, BUF = Lds::BUF;
-  constexpr int CPR = D / 8;         // 16-byte chunks per row
+  using Tl = PfTile<D>;
   constexpr int NDB = D / 16;        // 16-wide d blocks (QK^T k-steps)
   constexpr int NDO = D / 32;        // 32-wide d blocks (output tiles)
-  constexpr int LOADS = PF_BN * CPR / PF_THREADS;  // per tensor per thread
-  static_assert(LOADS * PF_THREADS == PF_BN * CPR, "tile must split evenly");
+  constexpr int TB = Tl::TILE_BYTES;
+  // LDS: K0 K1 V0 V1
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TB];
 
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * BUF];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int r32 = lane & 31, hh = lane >> 5;
 
   // workgroup -> (batch, kv head, q-block); causal: heaviest q-blocks first
@@ -109,6 +113,51 @@ prefill_kernel(PrefillParams p) {
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
   const int coff = p.T - p.S;
+
+  const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + coff) : p.T;
+  const int ntiles = (kv_end + PF_BN - 1) / PF_BN;
+  // K/V are bf16 in memory: they go to LDS unconverted
+  const unsigned char* kbase =
+      reinterpret_cast<const unsigned char*>(reinterpret_cast<const bf16*>(p.k) + b * p.ksb + kvh * p.ksh);
+  const unsigned char* vbase =
+      reinterpret_cast<const unsigned char*>(reinterpret_cast<const bf16*>(p.v) + b * p.vsb + kvh * p.vsh);
+  const int64_t krow_bytes = p.kss * 2, vrow_bytes = p.vss * 2;
+
+  // ---- tile loads: load instruction G (0 <= G < 4*LOADS) fills LDS bytes
+  // [G*1024, G*1024+1024) of the tile, lane t the 16 bytes at +16*t; wave w
+  // issues G = 4*m + w.  With that interleave a lane's row offset within its
+  // 4-row (8-row for D=64) group, and so its chunk swizzle, is the same for
+  // every m: the address is a wave-uniform base (tile, m) in SGPRs plus one
+  // loop-invariant 32-bit lane offset.  In a tile that runs past T the rows
+  // are clamped to T-1 instead (their scores are masked, so P = 0 there).
+  constexpr int RPI = 64 / Tl::CPR;  // rows per load instruction
+  const int row0 = wave * RPI + lane / Tl::CPR;  // row of instruction m: row0 + 4*RPI*m
+  const int pc0 = lane % Tl::CPR;
+  const uint32_t koff = (uint32_t)(row0 * krow_bytes) + Tl::k_chunk(row0, pc0) * 16;
+  const uint32_t voff = (uint32_t)(row0 * vrow_bytes) + Tl::v_chunk(row0, pc0) * 16;
+  auto load_tile = [&](const unsigned char* base, int64_t row_bytes, uint32_t off, int lds_off,
+                       int tile) {
+    const int lds_w = lds_off + wave * 1024;
+    if (tile * PF_BN + PF_BN <= p.T) {
+      const unsigned char* tb = base + (int64_t)tile * PF_BN * row_bytes;
+#pragma unroll
+      for (int m = 0; m < Tl::LOADS; ++m)
+        global_load_lds16(tb + m * 4 * RPI * row_bytes + off, smem + lds_w + m * 4096);
+    } else {
+      const uint32_t chunk_off = off - (uint32_t)(row0 * row_bytes);
+#pragma unroll
+      for (int m = 0; m < Tl::LOADS; ++m) {
+        const int key = min(tile * PF_BN + row0 + m * 4 * RPI, p.T - 1);
+        global_load_lds16(base + key * row_bytes + chunk_off, smem + lds_w + m * 4096);
+      }
+    }
+  };
+  auto load_k = [&](int tile, int buf) { load_tile(kbase, krow_bytes, koff, buf * TB, tile); };
+  auto load_v = [&](int tile, int buf) { load_tile(vbase, vrow_bytes, voff, (2 + buf) * TB, tile); };
+  // issue the first tiles before the Q work so their latency overlaps it
+  load_k(0, 0);
+  load_v(0, 0);
+  if (ntiles > 1) load_k(1, 1);
 
   // this lane's query row: column r32 of this wave's 32 rows
   const int R = wave * 32 + r32;
@@ -162,66 +211,72 @@ prefill_kernel(PrefillParams p) {
     for (int db = 0; db < NDB; ++db) qop[db] = to_bf16x8(xf[db]);
   }
 
-  const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + coff) : p.T;
-  const int ntiles = (kv_end + PF_BN - 1) / PF_BN;
-  const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.ksb + kvh * p.ksh;
-  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
-
-  // global -> register staging: thread owns 16-byte chunks c = tid + 256*i
-  bf16x8 kreg[LOADS], vreg[LOADS];
-  const bf16x8 zero8 = {};
-  auto load_tile = [&](int n0) {
+  // ---- per-lane LDS read offsets (bytes within a tile)
+  // K: MFMA row sigma(r32) (+32 for the second key block), chunk 2*db + hh
+  int k_off[NDB];
+  {
+    const int row = key_perm32(r32);
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * PF_THREADS;
-      const int key = n0 + c / CPR, ch = c % CPR;
-      const bool ok = key < p.T;
-      kreg[i] = ok ? Vec8<T>::load_bf16(kbase + (int64_t)key * p.kss + ch * 8) : zero8;
-      vreg[i] = ok ? Vec8<T>::load_bf16(vbase + (int64_t)key * p.vss + ch * 8) : zero8;
+    for (int db = 0; db < NDB; ++db) k_off[db] = row * Tl::ROW_BYTES + Tl::k_chunk(row, 2 * db + hh) * 16;
+  }
+  // V^T via transpose reads: lane group gi = lane/16, j = lane%16 reads row
+  // hh*8 + j/4 (+16*ks + 4*half), column dd*32 + (gi&1)*16 + 4*(j%4)
+  int v_off[NDO];
+  {
+    const int gi = lane >> 4, jj = lane & 15;
+    const int row = hh * 8 + (jj >> 2);
+#pragma unroll
+    for (int dd = 0; dd < NDO; ++dd) {
+      const int col = dd * 32 + (gi & 1) * 16 + 4 * (jj & 3);
+      v_off[dd] = row * Tl::ROW_BYTES + Tl::v_chunk(row, col / 8) * 16 + (col % 8) * 2;
+    }
+  }
+
+  auto qk = [&](int buf, floatx16& s0, floatx16& s1) {
+    s0 = floatx16{};
+    s1 = floatx16{};
+    const unsigned char* Kt = smem + buf * TB;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      bf16x8 a0 = *reinterpret_cast<const bf16x8*>(Kt + k_off[db]);
+      bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Kt + k_off[db] + 32 * Tl::ROW_BYTES);
+      s0 = mfma32(a0, qop[db], s0);
+      s1 = mfma32(a1, qop[db], s1);
     }
   };
-  auto store_tile = [&](int buf) {
-    bf16* Ks = smem + buf * BUF;
-    bf16* Vs = Ks + K_TILE;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * PF_THREADS;
-      *reinterpret_cast<bf16x8*>(Ks + (c / CPR) * KS + (c % CPR) * 8) = kreg[i];
-      *reinterpret_cast<bf16x8*>(Vs + (c / CPR) * VS + (c % CPR) * 8) = vreg[i];
-    }
-  };
-
-  // per-lane LDS offsets (elements within a buffer)
-  const int k_off = key_perm32(r32) * KS + hh * 8;
-  // V^T operand via transpose reads: lane group gi = lane/16, j = lane%16;
-  // source row hh*8 + j/4 (+ks*16 + 4*half), column (gi&1)*16 + 4*(j%4) (+dd*32)
-  const int gi = lane >> 4, jj = lane & 15;
-  const int v_off = K_TILE + (hh * 8 + (jj >> 2)) * VS + (gi & 1) * 16 + 4 * (jj & 3);
 
   float m_i = -INFINITY, l_i = 0.f;
   floatx16 oacc[NDO];
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) oacc[dd] = floatx16{};
 
-  load_tile(0);
-  store_tile(0);
+  // prologue: K0, V0 (and K1) in flight; S0
+  wait_vmcnt0();
   __syncthreads();
+  // S[j] lives in sA for even j and in sB for odd j (the loop is unrolled by
+  // two so neither the S registers nor the LDS buffer offsets need moving)
+  floatx16 sA[2], sB[2];
+  qk(0, sA[0], sA[1]);
 
-  for (int j = 0; j < ntiles; ++j) {
+  // One 64-key tile.  Order inside a step: barrier + next loads; mask and row
+  // max of S[j] (branches); then one branch-free block in which the MFMAs of
+  // S[j+1] = K[j+1] Q^T are interleaved with the exp/sum/convert of P[j]
+  // (sched_group_barrier keeps them interleaved, since a wave issues in
+  // order); then O += V[j]^T P[j].
+  auto step = [&](auto parity, auto has_next, int j) {
+    constexpr int P = decltype(parity)::value;       // == j & 1
+    constexpr bool NEXT = decltype(has_next)::value;  // j + 1 < ntiles
+    floatx16* s_cur = P ? sB : sA;
+    floatx16* s_next = P ? sA : sB;
     const int n0 = j * PF_BN;
-    const int buf = j & 1;
-    if (j + 1 < ntiles) load_tile(n0 + PF_BN);
-    const bf16* Bs = smem + buf * BUF;
-
-    // S^T = K Q^T for two 32-key blocks (chains interleaved)
-    floatx16 s[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(Bs + k_off + kb * 32 * KS + db * 16);
-        s[kb] = mfma32(a, qop[db], s[kb]);
-      }
+    // loads issued last step (K[j+1], V[j]) have landed; every wave is done
+    // with K[j] and V[j-1], so their buffers can be refilled
+    wait_vmcnt0();
+    __syncthreads();
+    if (NEXT) {
+      if (j + 2 < ntiles) load_k(j + 2, P);
+      load_v(j + 1, P ^ 1);
+    }
 
     // masking: keys past T, and (causal) keys past this row's frontier
     const bool need_mask = (n0 + PF_BN > p.T) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff);
@@ -232,7 +287,7 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = n0 + kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
-          if (key > lim) s[kb][i] = -INFINITY;
+          if (key > lim) s_cur[kb][i] = -INFINITY;
         }
     }
 
@@ -241,7 +296,7 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[kb][i]);
     mx = fmaxf(mx, shfl_xor_f(mx, 32)) * p.scale_log2;
     if (wave_any(mx > m_i + PF_RESCALE_LOG2)) {
       const float m_new = fmaxf(m_i, mx);
@@ -251,36 +306,83 @@ prefill_kernel(PrefillParams p) {
       for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
       m_i = m_new;
     }
-    // every row has seen key 0 by now, so m_i is finite
-    float rs = 0.f;
+
+    // ---- branch-free block, issued in a fixed order (sched_barrier fences)
+    // Phase B: NDB steps; step db reads the K operands of step db+1, issues
+    // the two MFMAs of S[j+1] for k-block db and computes 32/NDB of this
+    // lane's P values (exp2, row sum, bf16 pack) while those MFMAs run.
+    constexpr int PER = 32 / NDB;  // P values per step
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    floatx8 tv[4];
     bf16x8 pop[4];
+    bf16x8 ka0, ka1, kn0, kn1;
+    floatx16 sn0 = floatx16{}, sn1 = floatx16{};
+    const unsigned char* Kn = smem + (P ^ 1) * TB;
+    if (NEXT) {
+      ka0 = *reinterpret_cast<const bf16x8*>(Kn + k_off[0]);
+      ka1 = *reinterpret_cast<const bf16x8*>(Kn + k_off[0] + 32 * Tl::ROW_BYTES);
+    }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        floatx8 t;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pe = fast_exp2(s[kb][half * 8 + e] * p.scale_log2 - m_i);
-          rs += pe;
-          t[e] = pe;
+    for (int db = 0; db < NDB; ++db) {
+      if (NEXT) {
+        if (db + 1 < NDB) {
+          kn0 = *reinterpret_cast<const bf16x8*>(Kn + k_off[db + 1]);
+          kn1 = *reinterpret_cast<const bf16x8*>(Kn + k_off[db + 1] + 32 * Tl::ROW_BYTES);
         }
-        pop[kb * 2 + half] = to_bf16x8(t);
+        sn0 = mfma32(ka0, qop[db], sn0);
+        sn1 = mfma32(ka1, qop[db], sn1);
       }
-    l_i += rs;
-
-    // O^T += V^T P^T
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int dd = 0; dd < NDO; ++dd) {
-        const bf16* src = Bs + v_off + ks * 16 * VS + dd * 32;
-        bf16x8 a = lds_read_tr8(src, src + 4 * VS);
-        oacc[dd] = mfma32(a, pop[ks], oacc[dd]);
+      for (int u = 0; u < PER; ++u) {
+        const int idx = db * PER + u;  // 0..31: (kb, element)
+        const float pe = fast_exp2(s_cur[idx / 16][idx % 16] * p.scale_log2 - m_i);
+        acc[idx / 8] += pe;
+        tv[idx / 8][idx % 8] = pe;
+        if (idx % 8 == 7) pop[idx / 8] = to_bf16x8(tv[idx / 8]);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (NEXT) {
+        ka0 = kn0;
+        ka1 = kn1;
+      }
+    }
+    if (NEXT) {
+      s_next[0] = sn0;
+      s_next[1] = sn1;
+    }
+    l_i += (acc[0] + acc[1]) + (acc[2] + acc[3]);
 
-    if (j + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
+    // Phase C: O^T += V[j]^T P^T, next transpose-read operand prefetched
+    const unsigned char* Vt = smem + (2 + P) * TB;
+    auto vread = [&](int idx) {
+      const bf16* src = reinterpret_cast<const bf16*>(Vt + v_off[idx % NDO] + (idx / NDO) * 16 * Tl::ROW_BYTES);
+      return lds_read_tr8(src, src + 4 * D);
+    };
+    bf16x8 va = vread(0);
+#pragma unroll
+    for (int idx = 0; idx < 4 * NDO; ++idx) {
+      bf16x8 vn;
+      if (idx + 1 < 4 * NDO) vn = vread(idx + 1);
+      oacc[idx % NDO] = mfma32(va, pop[idx / NDO], oacc[idx % NDO]);
+      __builtin_amdgcn_sched_barrier(0);
+      va = vn;
+    }
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using Yes = std::integral_constant<bool, true>;
+  using No = std::integral_constant<bool, false>;
+  int j = 0;
+  for (; j + 2 < ntiles; j += 2) {
+    step(I0{}, Yes{}, j);
+    step(I1{}, Yes{}, j + 1);
+  }
+  if (ntiles - j == 2) {
+    step(I0{}, Yes{}, j);
+    step(I1{}, No{}, j + 1);
+  } else {
+    step(I0{}, No{}, j);
   }
 
   l_i += shfl_xor_f(l_i, 32);
@@ -338,10 +440,16 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   if (!nq_aligned16(q) || !nq_aligned16(k) || !nq_aligned16(v) || !nq_aligned16(o))
     return nq_fail(NQ_ERR_INVALID, "base pointers must be 16-byte aligned");
   const int esz = nq_dtype_size(dtype);
-  const int64_t* all[4] = {q_strides, k_strides, v_strides, o_strides};
-  for (const int64_t* s : all)
+  for (const int64_t* s : {q_strides, o_strides})
     for (int i = 0; i < 3; ++i)
-      if ((s[i] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "strides must be multiples of 16 bytes");
+      if ((s[i] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "q/o strides must be multiples of 16 bytes");
+  for (const int64_t* s : {k_strides, v_strides}) {  // bf16 rows
+    for (int i = 0; i < 3; ++i)
+      if ((s[i] * 2) % 16) return nq_fail(NQ_ERR_INVALID, "k/v strides must be multiples of 16 bytes");
+    // a tile's lane offsets (64 rows) are 32-bit
+    if (s[2] < 0 || (int64_t)PF_BN * s[2] * 2 >= (1LL << 31))
+      return nq_fail(NQ_ERR_UNSUPPORTED, "k/v sequence stride %lld too large", (long long)s[2]);
+  }
   if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
   PrefillParams p{};
