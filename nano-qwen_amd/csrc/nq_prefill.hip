@@ -105,11 +105,25 @@ prefill_kernel(PrefillParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int r32 = lane & 31, hh = lane >> 5;
 
-  // workgroup -> (batch, kv head, q-block); causal: heaviest q-blocks first
+  // workgroup -> (batch, kv head, q-block).  Workgroups are dealt to the 8
+  // XCDs round-robin (id % 8).  When the (batch, kv head) pairs split evenly
+  // over the XCDs and each pair has many q-blocks, XCD x works through its own
+  // pairs one after another, so the K/V of one pair (its L2 working set) is
+  // shared by all of that XCD's CUs; otherwise pairs are interleaved and the
+  // heaviest q-blocks of all pairs go first (better tail balance when each
+  // pair is only a few rounds of work).
   const int npairs = p.B * p.Hkv;
   const int L = blockIdx.x;
-  const int qblk = CAUSAL ? (p.nqb - 1 - L / npairs) : (L / npairs);
-  const int pair = L % npairs;
+  int qrank, pair;
+  if (npairs % 8 == 0 && p.nqb >= 128) {
+    const int xcd = L & 7, k = L >> 3;
+    pair = (k / p.nqb) * 8 + xcd;
+    qrank = k % p.nqb;
+  } else {
+    pair = L % npairs;
+    qrank = L / npairs;
+  }
+  const int qblk = CAUSAL ? (p.nqb - 1 - qrank) : qrank;
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
   const int coff = p.T - p.S;
