@@ -23,6 +23,7 @@ import torch
 from . import _lib
 
 __all__ = [
+    "KernelCall",
     "qk_norm_rope",
     "attention_prefill",
     "attention_decode",
@@ -101,6 +102,29 @@ def _tables(cos, sin, device):
     return c, s, c.shape[0]
 
 
+class KernelCall:
+    """A validated, fully bound call into libnqattn.so.
+
+    Built by the ops below with ``plan=True``: argument checks, output
+    allocation and the ctypes argument tuple are done once, so ``launch()``
+    is a single foreign call (for serving loops and benchmarks).  It keeps
+    every tensor it points at alive.  ``result`` holds what the op returns.
+    """
+
+    __slots__ = ("fn", "args", "stream_index", "name", "keep", "result")
+
+    def __init__(self, fn, args, stream_index, name, keep, result):
+        self.fn, self.args, self.stream_index = fn, list(args), stream_index
+        self.name, self.keep, self.result = name, keep, result
+
+    def launch(self, stream: Optional[torch.cuda.Stream] = None):
+        """Run the kernel(s) on ``stream`` (default: the stream current at planning time)."""
+        if stream is not None:
+            self.args[self.stream_index] = ctypes.c_void_p(stream.cuda_stream)
+        _lib.check(self.fn(*self.args), self.name)
+        return self.result
+
+
 # ---------------------------------------------------------------------------
 # QK-Norm + RoPE + cache placement
 # ---------------------------------------------------------------------------
@@ -113,7 +137,8 @@ def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = N
                  eps: float = 1e-6, cos: torch.Tensor, sin: torch.Tensor,
                  position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
                  pos_base: Optional[torch.Tensor] = None,
-                 kv_row_offset: int = 0, kv_row_base: Optional[torch.Tensor] = None):
+                 kv_row_offset: int = 0, kv_row_base: Optional[torch.Tensor] = None,
+                 plan: bool = False):
     """QK-Norm + rotate-half RoPE of Q/K rows and a row copy of V, in one launch.
 
     q: (B, Hq, S, D), k/v: (B, Hkv, S, D), any (b, h, s) strides.  Outputs
@@ -123,7 +148,8 @@ def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = N
     KVCache.update (model/attention.py:31-38).  Positions are
     ``position_ids[b, s]``, else ``pos_base[b] + s``, else ``pos_offset + s``
     (model/rope.py:123-129).  Norm weights None skip the norm.
-    Returns (q_out, k_out, v_out).
+    Returns (q_out, k_out, v_out), or with ``plan=True`` a KernelCall whose
+    ``launch()`` runs it.
     """
     ref = next(t for t in (q, k, v) if t is not None)
     _require_device(q, k, v, q_out, k_out, v_out)
@@ -164,7 +190,7 @@ def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = N
     qw, kw = _f32(q_weight, dev), _f32(k_weight, dev)
     lib = _lib.load()
     st = _lib.strides3
-    rc = lib.nq_qk_norm_rope(
+    args = (
         _ptr(q), st(q.stride()[:3]) if q is not None else None,
         _ptr(q_out), st(q_out.stride()[:3]) if q is not None else None,
         _ptr(k), st(k.stride()[:3]) if k is not None else None,
@@ -175,8 +201,9 @@ def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = N
         _ptr(qw), _ptr(kw), float(eps),
         _ptr(cos_t), _ptr(sin_t), max_pos,
         _ptr(pos), _ptr(pb), int(pos_offset), _ptr(rb), int(kv_row_offset), _stream(ref))
-    _lib.check(rc, "nq_qk_norm_rope")
-    return q_out, k_out, v_out
+    call = KernelCall(lib.nq_qk_norm_rope, args, len(args) - 1, "nq_qk_norm_rope",
+                      (q, k, v, cos_t, sin_t, pos, pb, rb, qw, kw), (q_out, k_out, v_out))
+    return call if plan else call.launch()
 
 
 # ---------------------------------------------------------------------------
@@ -189,7 +216,8 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                       position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
                       pos_base: Optional[torch.Tensor] = None,
                       causal: bool = True, sm_scale: Optional[float] = None,
-                      out: Optional[torch.Tensor] = None, return_lse: bool = False):
+                      out: Optional[torch.Tensor] = None, return_lse: bool = False,
+                      plan: bool = False):
     """GQA prefill attention with QK-Norm + RoPE of Q fused into its load.
 
     q: (B, Hq, S, D) pre-norm queries (norm/rope skipped when q_weight / cos
@@ -198,7 +226,8 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     Returns o shaped (B, Hq, S, D); by default it is a transposed view of a
     contiguous (B, S, Hq, D) buffer, so ``o.transpose(1, 2).reshape(B, S, -1)``
     (o_proj's input, model/attention.py:117) costs nothing.  With
-    ``return_lse`` also returns the fp32 (B, Hq, S) log-sum-exp.
+    ``return_lse`` also returns the fp32 (B, Hq, S) log-sum-exp.  With
+    ``plan=True`` returns a KernelCall whose ``launch()`` runs it.
     """
     _require_device(q, k, v, out)
     B, Hq, S, D = q.shape
@@ -227,14 +256,15 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     pb = _i32(pos_base, dev)
     qw = _f32(q_weight, dev)
     st = _lib.strides3
-    rc = _lib.load().nq_attn_prefill_fwd(
+    args = (
         _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
         _ptr(out), st(out.stride()[:3]), _ptr(lse),
         B, Hq, Hkv, S, T, D, dt, _ptr(qw), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
         _ptr(pos), _ptr(pb), int(pos_offset), int(bool(causal)),
         float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
-    _lib.check(rc, "nq_attn_prefill_fwd")
-    return (out, lse) if return_lse else out
+    call = KernelCall(_lib.load().nq_attn_prefill_fwd, args, len(args) - 1, "nq_attn_prefill_fwd",
+                      (q, k, v, cos_t, sin_t, pos, pb, qw), (out, lse) if return_lse else out)
+    return call if plan else call.launch()
 
 
 # ---------------------------------------------------------------------------
@@ -252,13 +282,15 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                      cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
                      q_pos: Optional[torch.Tensor] = None, q_pos0: int = -1,
                      sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                     workspace: Optional[torch.Tensor] = None, chunk: int = 0) -> torch.Tensor:
+                     workspace: Optional[torch.Tensor] = None, chunk: int = 0,
+                     plan: bool = False):
     """Single-token GQA decode against a ragged (B, Hkv, T_cap, D) cache.
 
     q: (B, Hq, D) or (B, Hq, 1, D) pre-norm query; keys [0, lens[b]) of the
     cache are attended (all ``max_len`` rows when lens is None).  The query
     is rotated at q_pos[b], else q_pos0, else lens[b] - 1 (q_pos0 < 0).
-    Returns (B, Hq, D).
+    Returns (B, Hq, D), or with ``plan=True`` a KernelCall whose ``launch()``
+    runs it.
     """
     _require_device(q, k_cache, v_cache, lens, out)
     if q.dim() == 4:
@@ -289,14 +321,15 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     q_str = (ctypes.c_int64 * 2)(q.stride(0), q.stride(1))
     o_str = (ctypes.c_int64 * 2)(out.stride(0), out.stride(1))
     st = _lib.strides3
-    rc = _lib.load().nq_attn_decode_fwd(
+    args = (
         _ptr(q), q_str, _ptr(k_cache), st(k_cache.stride()[:3]), _ptr(v_cache),
         st(v_cache.stride()[:3]), _ptr(lens_t), _ptr(out), o_str, _ptr(workspace), wbytes,
         B, Hq, Hkv, D, int(max_len), int(chunk), dt, _ptr(qw), float(eps),
         _ptr(cos_t), _ptr(sin_t), max_pos, _ptr(qp), int(q_pos0),
         float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
-    _lib.check(rc, "nq_attn_decode_fwd")
-    return out
+    call = KernelCall(_lib.load().nq_attn_decode_fwd, args, len(args) - 1, "nq_attn_decode_fwd",
+                      (q, k_cache, v_cache, lens_t, workspace, cos_t, sin_t, qp, qw, q_str, o_str), out)
+    return call if plan else call.launch()
 
 
 # ---------------------------------------------------------------------------
