@@ -122,7 +122,7 @@ class Decode:
         cos, sin = nq.build_tables(D, Tcap, 1e6)
         self.cos, self.sin = cos.to(device), sin.to(device)
         self.out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
-        nbytes = nq.decode_workspace_bytes(B, Hq, D, self.max_len)
+        nbytes = nq.decode_workspace_bytes(B, Hq, Hkv, D, self.max_len)
         self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         self.work = float(2 * Hkv * D * 2 * int(self.lens_cpu.sum()) + 2 * B * Hq * D * 2)
 

@@ -110,14 +110,16 @@ int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                         int causal, float sm_scale, void* stream);
 
 /*
- * Bytes of fp32 workspace nq_attn_decode_fwd needs for these sizes.
- * max_len bounds every lens[b]; chunk is the number of keys per split
- * (0 selects the library default).
+ * Bytes of fp32 workspace nq_attn_decode_fwd needs for these sizes (no
+ * counterpart in the reference, whose decode allocates inside torch).
+ * max_len bounds every lens[b].  chunk = 0 spreads the cache evenly over a
+ * persistent grid sized to the device; chunk > 0 gives every wave chunk keys
+ * (rounded up to a multiple of 32) of the concatenated rows instead.
  */
-int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int D, int max_len, int chunk);
+int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int max_len, int chunk);
 
 /*
- * Single-token decode attention against a ragged KV cache (split-K).
+ * Single-token decode attention against a ragged KV cache.
  *
  * Replaces model/attention.py:95-115 at S == 1 with a KVCache: the new
  * token's Q is QK-Normed and rotated in the kernel (q_weight / cos_tab may be
@@ -132,7 +134,7 @@ int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int D, int max_len, int ch
  *   every row, or lens[b] - 1 when q_pos0 < 0.
  * o: output (B, Hq, D) with strides {batch, head}.
  * workspace: device buffer of at least
- *   nq_attn_decode_workspace_bytes(B, Hq, D, max_len, chunk) bytes.
+ *   nq_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk) bytes.
  * Requires Hq / Hkv <= 16 or a multiple of 16.
  */
 int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const void* k_cache,

@@ -53,7 +53,7 @@ SIGNATURES = {
         _p, _p, _i32,                                # q_pos, q_pos_base, q_pos0
         _i32, _f32, _p,                              # causal, sm_scale, stream
     ]),
-    "nq_attn_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),
+    "nq_attn_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "nq_attn_decode_fwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p,             # q, k_cache, v_cache (+ strides)
         _p, _p, _i64p,                               # lens, o, o_strides

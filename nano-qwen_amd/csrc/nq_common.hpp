@@ -47,6 +47,10 @@ template <> struct Vec8<bf16> {
   __device__ __forceinline__ static bf16x8 load_bf16(const bf16* p) {
     return *reinterpret_cast<const bf16x8*>(p);
   }
+  // streaming (read-once) data: nontemporal load
+  __device__ __forceinline__ static bf16x8 load_bf16_nt(const bf16* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+  }
 };
 template <> struct Vec8<float> {
   __device__ __forceinline__ static floatx8 load_f32(const float* p) {
@@ -56,6 +60,11 @@ template <> struct Vec8<float> {
   }
   __device__ __forceinline__ static bf16x8 load_bf16(const float* p) {
     return __builtin_convertvector(load_f32(p), bf16x8);
+  }
+  __device__ __forceinline__ static bf16x8 load_bf16_nt(const float* p) {
+    floatx4 a = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
+    floatx4 b = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p + 4));
+    return __builtin_convertvector((floatx8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}), bf16x8);
   }
 };
 

@@ -1,4 +1,4 @@
-// Single-token GQA decode against a ragged KV cache, split-K, for gfx950.
+// Single-token GQA decode against a ragged KV cache, for gfx950.
 //
 // Replaces model/attention.py:95-115 at S == 1 with a KVCache (the decode
 // step driven by eval/generate.py:135): QK-Norm + RoPE of the new query
@@ -6,18 +6,32 @@
 // (attention.py:113: is_causal=False when a cache is present), and the GQA
 // expansion of attention.py:106-108 done by indexing, never materialised.
 //
-// Work decomposition
-//   grid (split, kv-head x head-group, batch).  A workgroup (4 waves) takes
-//   `chunk` consecutive keys of one (batch, kv head) and up to 16 query heads
-//   of that kv head's group; those 16 heads form the N side of
-//   v_mfma_f32_16x16x32_bf16 for both S^T = K Q^T (A = 16 keys x 32 dims,
-//   loaded straight from HBM in 16-byte pieces) and O^T += V^T P^T (A = V^T,
-//   staged through a per-wave LDS transpose).  Waves stride over 32-key steps
-//   of the chunk.  Each lane owns one head column, so the softmax reductions
-//   are two xor shuffles.  The four waves merge in LDS; a workgroup writes
-//   either the final row (single split) or an fp32 partial (O/l, m, l) that
-//   decode_merge_kernel combines.  Workgroups whose chunk starts past
-//   lens[b] exit at once, so the grid can be sized from max_len.
+// Work decomposition (a balanced partition of the whole cache)
+//   A "row" is one (batch b, kv head, group of up to 16 query heads); rows are
+//   ordered r = (b * Hkv + kv head) * NG + group and row r is cut into
+//   ceil(lens[b] / 32) steps of 32 keys.  Concatenating the steps of all rows
+//   gives N steps.  Each wave of the grid takes one contiguous range of that
+//   sequence: with chunk == 0 the N steps are split evenly over the resident
+//   waves (a persistent grid sized to the device), otherwise every wave takes
+//   chunk/32 steps.  Either way every wave streams the same number of bytes
+//   (to one step), whatever the spread of lens, and no workgroup is launched
+//   only to find its keys past lens[b].
+//
+//   A wave walks its range row by row.  For each row segment it QK-Norms and
+//   rotates the row's query heads (the N side of v_mfma_f32_16x16x32_bf16),
+//   then streams K and V 32 keys at a time: full 256-byte rows, nontemporal,
+//   one step ahead into registers, then into a wave-private LDS tile with an
+//   XOR swizzle, read back as the MFMA A operand (K, ds_read_b128) and as V^T
+//   (ds_read_b64_tr_b16); both read patterns are free of bank conflicts.  The
+//   online softmax is lane-local per head plus two xor shuffles.
+//
+//   A wave that covers a whole row writes the output row itself.  Otherwise
+//   it writes an fp32 partial (unnormalised O, running max m, sum l) to slot
+//   (wave + row) of the workspace: because ranges are contiguous and ordered,
+//   two (wave, row) pairs with the same sum cannot both occur, so at most
+//   waves + rows slots are used.  decode_merge_kernel recomputes which waves
+//   touched each row and combines their partials (and writes zeros for rows
+//   with no keys).
 //
 // The cache is read exactly once: HBM-bound at 16 FLOP/byte for G = 16.
 
@@ -26,9 +40,11 @@
 
 namespace nq {
 
-constexpr int DC_THREADS = 256;
-constexpr int DC_STEP = 32;             // keys per wave step
-constexpr int DC_DEFAULT_CHUNK = 1024;  // keys per split
+constexpr int DC_THREADS = 256;  // four independent waves
+constexpr int DC_WAVES = DC_THREADS / 64;
+constexpr int DC_STEP = 32;      // keys per wave step
+constexpr int DC_WG_PER_CU = 2;  // resident workgroups per CU for the persistent grid
+constexpr int DC_MAX_WAVES = 2048;  // persistent grid cap: 256 CUs x 2 workgroups x 4 waves
 
 struct DecodeParams {
   const void* q;
@@ -40,8 +56,8 @@ struct DecodeParams {
   const int32_t* lens;
   void* o;
   int64_t osb, osh;
-  float* ws_o;   // (B, Hq, nsplit, D) normalised partial outputs
-  float* ws_ml;  // (B, Hq, nsplit, 2)  (m in log2 units, l)
+  float* ws_o;   // (slots, 16, D) unnormalised partial outputs
+  float* ws_ml;  // (slots, 16, 2) running max (log2 units) and sum
   const float* qw;
   float eps;
   const float* cos_tab;
@@ -49,280 +65,462 @@ struct DecodeParams {
   int max_pos;
   const int32_t* q_pos;
   int q_pos0;
-  int B, Hq, Hkv, G, NG, nsplit, chunk, max_len;
+  int B, Hq, Hkv, G, NG, max_len;
+  int rows_per_batch;  // Hkv * NG
+  int nwaves;          // waves launched
+  int span;            // steps per wave; 0 = split N evenly over nwaves
   float scale_log2;
 };
 
-template <int D, typename T>
-__global__ void __attribute__((amdgpu_flat_work_group_size(DC_THREADS, DC_THREADS)))
-decode_split_kernel(DecodeParams p) {
-  constexpr int NDQ = D / 32;         // 32-wide d blocks (QK^T k-steps)
-  constexpr int NDO = D / 16;         // 16-wide d blocks (output tiles)
-  constexpr int CPR = D / 8;          // 16-byte chunks per V row
-  constexpr int VS = D + 16;          // V row stride (elements) in LDS: +32 B
-  constexpr int V_LOADS = DC_STEP * CPR / 64;  // 16-byte V loads per lane per step
-  constexpr int WAVE_LDS = DC_STEP * VS;       // bf16 elements per wave
-  constexpr int COMB_F = 4 * 16 * D + 2 * 4 * 16;  // floats for the wave merge
-  constexpr int LDS_BYTES = (4 * WAVE_LDS * 2 > COMB_F * 4) ? 4 * WAVE_LDS * 2 : COMB_F * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char smem_raw[LDS_BYTES];
+// LDS tile of DC_STEP rows (keys) x D bf16, 16-byte chunks XOR-swizzled per row.
+template <int D>
+struct DcTile {
+  static constexpr int RB = 2 * D;                 // bytes per row
+  static constexpr int CPR = D / 8;                // 16-byte chunks per row
+  static constexpr int RPB = 256 / RB;             // rows per 256-byte bank row
+  static constexpr int BYTES = DC_STEP * RB;       // one K or V tile
+  static constexpr int RPI = 64 / CPR;             // rows per 64-lane load
+  static constexpr int LOADS = DC_STEP / RPI;      // 16-byte pieces per lane per tile
+  // K: a ds_read_b128 of one chunk from 16 consecutive rows hits 16 distinct
+  // 16-byte bank groups.
+  __device__ static int kswz(int row) { return (row / RPB) % CPR; }
+  // V: a transpose read of 32 bytes from 8 consecutive rows hits 8 distinct
+  // 32-byte bank groups.
+  __device__ static int vswz(int row) { return ((row / RPB) % (CPR / 2)) * 2; }
+};
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y / p.NG, hgi = blockIdx.y % p.NG;
-  const int b = blockIdx.z;
-  // lens[b] is clamped to max_len (the caller guarantees max_len <= T_cap), so
-  // no key past the cache capacity is ever read.
-  const int len = p.lens ? min(p.lens[b], p.max_len) : p.max_len;
-  const int s0 = split * p.chunk;
-  if (len <= 0) {
-    // empty row: defined output (zeros) instead of an unwritten buffer
-    if (split == 0) {
-      for (int idx = threadIdx.x; idx < 16 * D; idx += DC_THREADS) {
-        const int ghq = hgi * 16 + idx / D;
-        if (ghq < p.G)
-          (reinterpret_cast<T*>(p.o) + b * p.osb + (kvh * p.G + ghq) * p.osh)[idx % D] = static_cast<T>(0.f);
-      }
-    }
-    return;
+// K/V pieces come through buffer loads: the descriptor's range ends after the
+// last key of the segment, so the hardware returns zeros for keys past it (no
+// per-lane branches, and NaN-poisoned or unallocated rows are never read).
+// aux = 2 marks the loads nontemporal (each cache byte is read once).
+constexpr int DC_BUF_FLAGS = 0x00020000;  // gfx9 raw-buffer descriptor word 3
+constexpr int DC_AUX_NT = 2;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dc_buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, DC_BUF_FLAGS);
+}
+
+// Storage type -> 8-element piece held between the HBM load and the LDS store.
+template <typename T> struct Piece;
+template <> struct Piece<bf16> {
+  typedef bf16x8 type;
+  __device__ __forceinline__ static type load(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, DC_AUX_NT));
   }
-  if (s0 >= len) return;
-  const int s1 = min(len, s0 + p.chunk);
-  const int nsplit_b = (len + p.chunk - 1) / p.chunk;
+  __device__ __forceinline__ static bf16x8 to_bf16(type v) { return v; }
+};
+template <> struct Piece<float> {
+  typedef floatx8 type;
+  __device__ __forceinline__ static type load(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    floatx4 a = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, DC_AUX_NT));
+    floatx4 b = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, DC_AUX_NT));
+    return floatx8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  }
+  __device__ __forceinline__ static bf16x8 to_bf16(type v) { return __builtin_convertvector(v, bf16x8); }
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------- schedule
+__device__ __forceinline__ int batch_len(const DecodeParams& p, int b) {
+  return p.lens ? min(p.lens[b], p.max_len) : p.max_len;
+}
+__device__ __forceinline__ int batch_steps(const DecodeParams& p, int b) {
+  const int len = batch_len(p, b);
+  return len > 0 ? (len + DC_STEP - 1) / DC_STEP : 0;
+}
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ int64_t lane_value_i64(int64_t v, int src) {
+  const int lo = __builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, src);
+  const int hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), src);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Total number of steps N over all rows (same value in every lane).
+__device__ int64_t total_steps(const DecodeParams& p, int lane) {
+  int64_t acc = 0;
+  for (int base = 0; base < p.B; base += 64) {
+    const int b = base + lane;
+    if (b < p.B) acc += batch_steps(p, b);
+  }
+  return wave_sum_i64(acc) * p.rows_per_batch;
+}
+
+// Steps before the first row of batch b.
+__device__ int64_t steps_before(const DecodeParams& p, int lane, int b) {
+  int64_t acc = 0;
+  for (int base = 0; base < b; base += 64) {
+    const int bb = base + lane;
+    if (bb < b) acc += batch_steps(p, bb);
+  }
+  return wave_sum_i64(acc) * p.rows_per_batch;
+}
+
+// The batch whose rows hold global step q (q < N), and the steps before it.
+__device__ void find_batch(const DecodeParams& p, int lane, int64_t q, int& b_out, int64_t& before) {
+  int64_t run = 0;
+  for (int base = 0; base < p.B; base += 64) {
+    const int b = base + lane;
+    const int64_t v = b < p.B ? (int64_t)batch_steps(p, b) * p.rows_per_batch : 0;
+    int64_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int64_t t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    const int64_t excl = run + incl - v;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(v > 0 && excl <= q && q < excl + v);
+    if (hit) {
+      const int src = __builtin_ctzll(hit);
+      b_out = base + src;
+      before = lane_value_i64(excl, src);
+      return;
+    }
+    run += lane_value_i64(incl, 63);
+  }
+  b_out = p.B - 1;  // not reached for q < N
+  before = run;
+}
+
+// Effective number of waves of the balanced split (never more than N).
+__device__ __forceinline__ int64_t waves_used(const DecodeParams& p, int64_t N) {
+  return p.span > 0 ? (N + p.span - 1) / p.span : min((int64_t)p.nwaves, N);
+}
+// First global step of wave w.
+__device__ __forceinline__ int64_t wave_begin(const DecodeParams& p, int64_t N, int64_t We, int64_t w) {
+  return p.span > 0 ? min(N, w * p.span) : w * N / We;
+}
+// The wave whose range holds global step s.
+__device__ __forceinline__ int64_t wave_of(const DecodeParams& p, int64_t N, int64_t We, int64_t s) {
+  return p.span > 0 ? s / p.span : ((s + 1) * We - 1) / N;
+}
+
+// ---------------------------------------------------------------- kernels
+template <int D, typename T, bool PIPE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(DC_THREADS, DC_THREADS), amdgpu_waves_per_eu(DC_WG_PER_CU)))
+decode_stream_kernel(DecodeParams p) {
+  using L = DcTile<D>;
+  using P8 = Piece<T>;
+  constexpr int NDQ = D / 32;  // 32-wide d blocks (QK^T k-steps)
+  constexpr int NDO = D / 16;  // 16-wide d blocks (output tiles)
+  __shared__ __attribute__((aligned(16))) unsigned char smem[DC_WAVES * 2 * L::BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t w = (int64_t)blockIdx.x * DC_WAVES + wave;
+
+  const int64_t N = lane_value_i64(total_steps(p, lane), 0);
+  if (N == 0) return;
+  const int64_t We = waves_used(p, N);
+  if (w >= We) return;
+  const int64_t q0 = wave_begin(p, N, We, w), q1 = wave_begin(p, N, We, w + 1);
+  if (q0 >= q1) return;
+
+  int b;
+  int64_t before;
+  find_batch(p, lane, q0, b, before);
+  int nb = uniform(batch_steps(p, b));
+  int j = (int)((q0 - before) / nb);   // row within the batch
+  int ls = (int)((q0 - before) % nb);  // first step within the row
+
   const int c16 = lane & 15, grp = lane >> 4;
-  const int gh = hgi * 16 + c16;
-  const bool hvalid = gh < p.G;
-  const int head = kvh * p.G + (hvalid ? gh : 0);
+  unsigned char* kt = smem + wave * 2 * L::BYTES;
+  unsigned char* vt = kt + L::BYTES;
 
-  // ---- Q operand (B of S^T = K Q^T): lane holds Q[head c16][dq*32 + grp*8 + e]
-  bf16x8 qop[NDQ];
-  {
+  // loop-invariant LDS offsets
+  const int lrow = lane / L::CPR, lc = lane % L::CPR;  // piece (row, chunk) for loads
+  int kwa[L::LOADS], vwa[L::LOADS];
+#pragma unroll
+  for (int i = 0; i < L::LOADS; ++i) {
+    const int row = i * L::RPI + lrow;
+    kwa[i] = row * L::RB + ((lc ^ L::kswz(row)) << 4);
+    vwa[i] = row * L::RB + ((lc ^ L::vswz(row)) << 4);
+  }
+  // K operand (kb, dq): row kb*16 + c16, chunk dq*4 + grp -> koff ^ (dq << 6) + kb*16*RB
+  const int koff = c16 * L::RB + ((grp ^ L::kswz(c16)) << 4);
+  // V^T operand (half h, dd): source row 16h + 4grp + jj/4, column dd*16 + 4*(jj%4)
+  const int jj = lane & 15;
+  const int vrow = 4 * grp + (jj >> 2);
+  const int voff = vrow * L::RB + ((L::vswz(vrow) >> 1) << 5) + (jj & 3) * 8;
+
+  int64_t q = q0;
+  while (true) {
+    const int len = uniform(batch_len(p, b));
+    const int kvh = j / p.NG, hg = j % p.NG;
+    const int nseg = (int)min((int64_t)(nb - ls), q1 - q);
+    const bool whole = ls == 0 && nseg == nb;
+    const int kbeg = ls * DC_STEP;
+    const int kend = min(len, (ls + nseg) * DC_STEP);
+
+    // ---- query-side loads first (so waiting for them does not wait for K/V)
+    const int gh = hg * 16 + c16;
+    const bool hvalid = gh < p.G;
+    const int head = kvh * p.G + (hvalid ? gh : 0);
     const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh;
-    floatx8 xf[NDQ];
+    floatx8 xf[NDQ], wq[NDQ], cs[NDQ / 2], sn[NDQ / 2];
 #pragma unroll
     for (int dq = 0; dq < NDQ; ++dq) xf[dq] = Vec8<T>::load_f32(qrow + dq * 32 + grp * 8);
     if (p.qw) {
-      float ss = 0.f;
 #pragma unroll
-      for (int dq = 0; dq < NDQ; ++dq)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += xf[dq][e] * xf[dq][e];
-      ss += shfl_xor_f(ss, 16);
-      ss += shfl_xor_f(ss, 32);
-      const float r = rsqrtf(ss / (float)D + p.eps);
-#pragma unroll
-      for (int dq = 0; dq < NDQ; ++dq) {
-        floatx8 w = Vec8<float>::load_f32(p.qw + dq * 32 + grp * 8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xf[dq][e] = xf[dq][e] * r * w[e];
-      }
+      for (int dq = 0; dq < NDQ; ++dq) wq[dq] = Vec8<float>::load_f32(p.qw + dq * 32 + grp * 8);
     }
     if (p.cos_tab) {
-      const int pos = clamp_pos(p.q_pos ? p.q_pos[b] : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos);
+      const int pos = clamp_pos(p.q_pos ? uniform(p.q_pos[b]) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos);
       const float* ct = p.cos_tab + (int64_t)pos * (D / 2);
       const float* st = p.sin_tab + (int64_t)pos * (D / 2);
 #pragma unroll
       for (int dq = 0; dq < NDQ / 2; ++dq) {
-        floatx8 c = Vec8<float>::load_f32(ct + dq * 32 + grp * 8);
-        floatx8 s = Vec8<float>::load_f32(st + dq * 32 + grp * 8);
-        floatx8 x1 = xf[dq], x2 = xf[dq + NDQ / 2];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          xf[dq][e] = x1[e] * c[e] - x2[e] * s[e];
-          xf[dq + NDQ / 2][e] = x2[e] * c[e] + x1[e] * s[e];
-        }
+        cs[dq] = Vec8<float>::load_f32(ct + dq * 32 + grp * 8);
+        sn[dq] = Vec8<float>::load_f32(st + dq * 32 + grp * 8);
       }
     }
-#pragma unroll
-    for (int dq = 0; dq < NDQ; ++dq) qop[dq] = hvalid ? to_bf16x8(xf[dq]) : bf16x8{};
-  }
 
-  const T* kbase = reinterpret_cast<const T*>(p.kc) + b * p.ksb + kvh * p.ksh;
-  const T* vbase = reinterpret_cast<const T*>(p.vc) + b * p.vsb + kvh * p.vsh;
-  bf16* Vs = reinterpret_cast<bf16*>(smem_raw) + wave * WAVE_LDS;
-  const bf16x8 zero8 = {};
-  // V^T operand via transpose reads: lane group grp, j = lane%16: source row
-  // 4*grp + j/4 (+16 for the second half), column 4*(j%4) (+dd*16).  Rows
-  // 16*half + 4*grp + [0,4) are exactly the keys of this lane's P values.
-  const int jj = lane & 15;
-  const int v_off = (4 * grp + (jj >> 2)) * VS + 4 * (jj & 3);
+    // ---- K/V of this (batch, kv head): keys [0, kend) are in range
+    const int esz = (int)sizeof(T);
+    const __amdgpu_buffer_rsrc_t krs = dc_buffer(reinterpret_cast<const T*>(p.kc) + b * p.ksb + kvh * p.ksh,
+                                                 (uint32_t)((int64_t)(kend - 1) * p.kst * esz + D * esz));
+    const __amdgpu_buffer_rsrc_t vrs = dc_buffer(reinterpret_cast<const T*>(p.vc) + b * p.vsb + kvh * p.vsh,
+                                                 (uint32_t)((int64_t)(kend - 1) * p.vst * esz + D * esz));
+    const int kvo = (int)(lrow * p.kst * esz) + lc * 8 * esz;
+    const int vvo = (int)(lrow * p.vst * esz) + lc * 8 * esz;
+    const int kstep = (int)(L::RPI * p.kst * esz), vstep = (int)(L::RPI * p.vst * esz);
+    typename P8::type kr[L::LOADS], vr[L::LOADS];
+    auto load = [&](int k0) {
+      const int ks = (int)(k0 * p.kst * esz), vs = (int)(k0 * p.vst * esz);
+#pragma unroll
+      for (int i = 0; i < L::LOADS; ++i) {
+        kr[i] = P8::load(krs, kvo, ks + i * kstep);
+        vr[i] = P8::load(vrs, vvo, vs + i * vstep);
+      }
+    };
+    load(kbeg);
 
-  float m_i = -INFINITY, l_i = 0.f;
-  floatx4 oacc[NDO];
+    // ---- Q operand (B of S^T = K Q^T): lane holds Q[head c16][dq*32 + grp*8 + e]
+    bf16x8 qop[NDQ];
+    {
+      if (p.qw) {
+        float ss = 0.f;
 #pragma unroll
-  for (int dd = 0; dd < NDO; ++dd) oacc[dd] = floatx4{};
-
-  const int nsteps = (s1 - s0 + DC_STEP - 1) / DC_STEP;
-  for (int t = wave; t < nsteps; t += 4) {
-    const int k0 = s0 + t * DC_STEP;
-    // K as MFMA A operand: block kb, row r holds key kb*16 + r
-    bf16x8 ka[2][NDQ];
+        for (int dq = 0; dq < NDQ; ++dq)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int key = k0 + kb * 16 + c16;
-      const bool ok = key < s1;
+          for (int e = 0; e < 8; ++e) ss += xf[dq][e] * xf[dq][e];
+        ss += shfl_xor_f(ss, 16);
+        ss += shfl_xor_f(ss, 32);
+        const float r = rsqrtf(ss / (float)D + p.eps);
 #pragma unroll
-      for (int dq = 0; dq < NDQ; ++dq)
-        ka[kb][dq] = ok ? Vec8<T>::load_bf16(kbase + (int64_t)key * p.kst + dq * 32 + grp * 8) : zero8;
+        for (int dq = 0; dq < NDQ; ++dq)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xf[dq][e] = xf[dq][e] * r * wq[dq][e];
+      }
+      if (p.cos_tab) {
+#pragma unroll
+        for (int dq = 0; dq < NDQ / 2; ++dq) {
+          floatx8 x1 = xf[dq], x2 = xf[dq + NDQ / 2];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            xf[dq][e] = x1[e] * cs[dq][e] - x2[e] * sn[dq][e];
+            xf[dq + NDQ / 2][e] = x2[e] * cs[dq][e] + x1[e] * sn[dq][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int dq = 0; dq < NDQ; ++dq) qop[dq] = hvalid ? to_bf16x8(xf[dq]) : bf16x8{};
     }
-    // V rows, whole rows per 16 lanes: chunk c = lane + 64*i
-    bf16x8 vr[V_LOADS];
-#pragma unroll
-    for (int i = 0; i < V_LOADS; ++i) {
-      const int c = lane + 64 * i;
-      const int key = k0 + c / CPR;
-      vr[i] = key < s1 ? Vec8<T>::load_bf16(vbase + (int64_t)key * p.vst + (c % CPR) * 8) : zero8;
-    }
 
-    floatx4 sc[2];
+    float m_i = -INFINITY, l_i = 0.f;
+    floatx4 oacc[NDO];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sc[kb] = floatx4{};
+    for (int dd = 0; dd < NDO; ++dd) oacc[dd] = floatx4{};
+
+    for (int s = 0; s < nseg; ++s) {
+      const int k0 = kbeg + s * DC_STEP;
+      // registers -> LDS (in-order LDS within the wave: the previous step's
+      // reads of this tile have been served before these writes)
 #pragma unroll
-      for (int dq = 0; dq < NDQ; ++dq) sc[kb] = mfma16(ka[kb][dq], qop[dq], sc[kb]);
-    }
-    if (k0 + DC_STEP > s1) {
+      for (int i = 0; i < L::LOADS; ++i) {
+        *reinterpret_cast<bf16x8*>(kt + kwa[i]) = P8::to_bf16(kr[i]);
+        *reinterpret_cast<bf16x8*>(vt + vwa[i]) = P8::to_bf16(vr[i]);
+      }
+      if (PIPE && s + 1 < nseg) load(k0 + DC_STEP);
+
+      floatx4 sc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sc[kb] = floatx4{};
+#pragma unroll
+        for (int dq = 0; dq < NDQ; ++dq) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + ((koff ^ (dq << 6)) + kb * 16 * L::RB));
+          sc[kb] = mfma16(a, qop[dq], sc[kb]);
+        }
+      }
+      if (k0 + DC_STEP > kend) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (k0 + kb * 16 + grp * 4 + i >= kend) sc[kb][i] = -INFINITY;
+      }
+      float mx = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (k0 + kb * 16 + grp * 4 + i >= s1) sc[kb][i] = -INFINITY;
-    }
-
-    float mx = -INFINITY;
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][i]);
+      mx = fmaxf(mx, shfl_xor_f(mx, 16));
+      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+      // every step holds at least one key < kend, so m_new is finite
+      const float m_new = fmaxf(m_i, mx * p.scale_log2);
+      const float alpha = fast_exp2(m_i - m_new);
+      floatx8 pf;
+      float rs = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][i]);
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float m_new = fmaxf(m_i, mx * p.scale_log2);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_i - m_use);
-    floatx8 pf;
-    float rs = 0.f;
+        for (int i = 0; i < 4; ++i) {
+          const float pe = fast_exp2(sc[kb][i] * p.scale_log2 - m_new);
+          pf[kb * 4 + i] = pe;
+          rs += pe;
+        }
+      const bf16x8 pop = to_bf16x8(pf);
+      l_i = l_i * alpha + rs;
+      m_i = m_new;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pe = fast_exp2(sc[kb][i] * p.scale_log2 - m_use);
-        pf[kb * 4 + i] = pe;
-        rs += pe;
+      for (int dd = 0; dd < NDO; ++dd) {
+        oacc[dd] *= alpha;
+        const unsigned char* src = vt + (voff ^ (dd << 5));
+        const bf16x8 a = lds_read_tr8(reinterpret_cast<const bf16*>(src),
+                                      reinterpret_cast<const bf16*>(src + 16 * L::RB));
+        oacc[dd] = mfma16(a, pop, oacc[dd]);
       }
-    const bf16x8 pop = to_bf16x8(pf);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-#pragma unroll
-    for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
-
-    // V rows into this wave's LDS slab (row-major), read back transposed
-#pragma unroll
-    for (int i = 0; i < V_LOADS; ++i) {
-      const int c = lane + 64 * i;
-      *reinterpret_cast<bf16x8*>(Vs + (c / CPR) * VS + (c % CPR) * 8) = vr[i];
+      if (!PIPE && s + 1 < nseg) load(k0 + DC_STEP);
     }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int dd = 0; dd < NDO; ++dd) {
-      const bf16* src = Vs + v_off + dd * 16;
-      bf16x8 a = lds_read_tr8(src, src + 16 * VS);
-      oacc[dd] = mfma16(a, pop, oacc[dd]);
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
 
-  // ---- merge the four waves through LDS
-  l_i += shfl_xor_f(l_i, 16);
-  l_i += shfl_xor_f(l_i, 32);
-  __syncthreads();
-  float* co = reinterpret_cast<float*>(smem_raw);        // [wave][16][D]
-  float* cm = co + 4 * 16 * D;                          // [wave][16]
-  float* cl = cm + 4 * 16;                              // [wave][16]
-  if (grp == 0) {
-    cm[wave * 16 + c16] = m_i;
-    cl[wave * 16 + c16] = l_i;
-  }
+    // ---- flush the segment
+    l_i += shfl_xor_f(l_i, 16);
+    l_i += shfl_xor_f(l_i, 32);
+    const int64_t r = ((int64_t)b * p.Hkv + kvh) * p.NG + hg;
+    if (whole) {
+      if (hvalid) {
+        T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (int64_t)(kvh * p.G + gh) * p.osh;
+        const float inv = 1.0f / l_i;
 #pragma unroll
-  for (int dd = 0; dd < NDO; ++dd)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) co[(wave * 16 + c16) * D + dd * 16 + grp * 4 + i] = oacc[dd][i];
-  __syncthreads();
-
-  const bool single = nsplit_b == 1;
-  for (int idx = tid; idx < 16 * D; idx += DC_THREADS) {
-    const int hq = idx / D, d = idx - hq * D;
-    const int ghq = hgi * 16 + hq;
-    if (ghq >= p.G) continue;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, cm[w * 16 + hq]);
-    float wsum = 0.f, osum = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float sc = fast_exp2(cm[w * 16 + hq] - M);
-      wsum += cl[w * 16 + hq] * sc;
-      osum += co[(w * 16 + hq) * D + d] * sc;
-    }
-    const int hglob = kvh * p.G + ghq;
-    if (single) {
-      T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + hglob * p.osh;
-      orow[d] = static_cast<T>(osum / wsum);
+        for (int dd = 0; dd < NDO; ++dd) store4<T>(orow + dd * 16 + grp * 4, oacc[dd] * inv);
+      }
     } else {
-      const int64_t slot = ((int64_t)b * p.Hq + hglob) * p.nsplit + split;
-      p.ws_o[slot * D + d] = osum / wsum;
-      if (d == 0) {
-        p.ws_ml[slot * 2 + 0] = M;
-        p.ws_ml[slot * 2 + 1] = wsum;
-      }
+      const int64_t slot = w + r;
+      float* so = p.ws_o + (slot * 16 + c16) * D;
+#pragma unroll
+      for (int dd = 0; dd < NDO; ++dd) *reinterpret_cast<floatx4*>(so + dd * 16 + grp * 4) = oacc[dd];
+      if (grp == 0) *reinterpret_cast<floatx2*>(p.ws_ml + (slot * 16 + c16) * 2) = floatx2{m_i, l_i};
+    }
+
+    q += nseg;
+    if (q >= q1) break;
+    ls = 0;
+    if (++j == p.rows_per_batch) {
+      j = 0;
+      do nb = uniform(batch_steps(p, ++b)); while (nb == 0 && b + 1 < p.B);  // q < N: a batch with keys follows
     }
   }
 }
 
-// One workgroup per (batch, query head); one lane per output element.
+// One workgroup per row (batch, kv head, head group): combines the partials
+// of the waves that covered the row, or writes zeros for a row without keys.
 template <int D, typename T>
-__global__ void __launch_bounds__(D) decode_merge_kernel(DecodeParams p) {
-  const int b = blockIdx.y, h = blockIdx.x, d = threadIdx.x;
-  const int len = p.lens ? min(p.lens[b], p.max_len) : p.max_len;
-  const int ns = (len + p.chunk - 1) / p.chunk;
-  if (ns <= 1) return;
-  const int64_t base = ((int64_t)b * p.Hq + h) * p.nsplit;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, p.ws_ml[(base + s) * 2]);
-  float wsum = 0.f, osum = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float w = p.ws_ml[(base + s) * 2 + 1] * fast_exp2(p.ws_ml[(base + s) * 2] - M);
-    wsum += w;
-    osum += w * p.ws_o[(base + s) * D + d];
+__global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = blockIdx.x;
+  const int b = (int)(r / p.rows_per_batch), j = (int)(r % p.rows_per_batch);
+  const int kvh = j / p.NG, hg = j % p.NG;
+  const int nb = batch_steps(p, b);
+  T* obase = reinterpret_cast<T*>(p.o) + b * p.osb;
+  if (nb == 0) {
+    for (int idx = threadIdx.x; idx < 16 * D; idx += DC_THREADS) {
+      const int gh = hg * 16 + idx / D;
+      if (gh < p.G) obase[(int64_t)(kvh * p.G + gh) * p.osh + idx % D] = static_cast<T>(0.f);
+    }
+    return;
   }
-  T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + h * p.osh;
-  orow[d] = static_cast<T>(osum / wsum);
+  const int64_t N = total_steps(p, lane);
+  const int64_t We = waves_used(p, N);
+  const int64_t first = steps_before(p, lane, b) + (int64_t)j * nb;
+  const int64_t wf = wave_of(p, N, We, first), wl = wave_of(p, N, We, first + nb - 1);
+  if (wf == wl) return;  // one wave covered the row and wrote it
+  for (int idx = threadIdx.x; idx < 16 * D; idx += DC_THREADS) {
+    const int hq = idx / D, d = idx % D;
+    const int gh = hg * 16 + hq;
+    if (gh >= p.G) continue;
+    float M = -INFINITY;
+    for (int64_t w = wf; w <= wl; ++w) M = fmaxf(M, p.ws_ml[((w + r) * 16 + hq) * 2]);
+    float wsum = 0.f, osum = 0.f;
+    for (int64_t w = wf; w <= wl; ++w) {
+      const int64_t slot = w + r;
+      const float sc = fast_exp2(p.ws_ml[(slot * 16 + hq) * 2] - M);
+      wsum += p.ws_ml[(slot * 16 + hq) * 2 + 1] * sc;
+      osum += p.ws_o[(slot * 16 + hq) * D + d] * sc;
+    }
+    obase[(int64_t)(kvh * p.G + gh) * p.osh + d] = static_cast<T>(osum / wsum);
+  }
+}
+
+static int dc_span(int chunk) { return chunk > 0 ? (chunk + DC_STEP - 1) / DC_STEP : 0; }
+
+// Waves the grid launches (an upper bound of the waves that take steps).
+static int64_t dc_waves(int B, int Hkv, int NG, int max_len, int chunk) {
+  const int span = dc_span(chunk);
+  if (span == 0) return DC_MAX_WAVES;
+  const int64_t upper = (int64_t)B * Hkv * NG * ((max_len + DC_STEP - 1) / DC_STEP);
+  return ((upper + span - 1) / span + DC_WAVES - 1) / DC_WAVES * DC_WAVES;
+}
+
+static int64_t dc_workspace(int B, int Hq, int Hkv, int D, int max_len, int chunk) {
+  const int NG = (Hq / Hkv + 15) / 16;
+  const int64_t slots = dc_waves(B, Hkv, NG, max_len, chunk) + (int64_t)B * Hkv * NG;
+  return slots * 16 * (D + 2) * (int64_t)sizeof(float);
 }
 
 template <int D, typename T>
-static hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
-  dim3 grid((unsigned)p.nsplit, (unsigned)(p.Hkv * p.NG), (unsigned)p.B);
-  hipLaunchKernelGGL((decode_split_kernel<D, T>), grid, dim3(DC_THREADS), 0, st, p);
+static hipError_t launch_decode(DecodeParams p, hipStream_t st) {
+  auto kern = decode_stream_kernel<D, T, sizeof(T) == 2>;
+  if (p.span == 0) {
+    // persistent grid: as many waves as stay resident at once (<= DC_MAX_WAVES),
+    // worked out once per device
+    static int resident[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int waves = (dev >= 0 && dev < 64) ? __atomic_load_n(&resident[dev], __ATOMIC_RELAXED) : 0;
+    if (waves == 0) {
+      int cus = 0, per_cu = 0;
+      e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e == hipSuccess)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), DC_THREADS, 0);
+      if (e != hipSuccess) return e;
+      const int64_t per = per_cu < 1 ? 1 : (per_cu > DC_WG_PER_CU ? DC_WG_PER_CU : per_cu);
+      const int64_t all = (int64_t)cus * per * DC_WAVES;
+      waves = (int)(all < DC_MAX_WAVES ? all : DC_MAX_WAVES);
+      if (dev >= 0 && dev < 64) __atomic_store_n(&resident[dev], waves, __ATOMIC_RELAXED);
+    }
+    p.nwaves = waves;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(p.nwaves / DC_WAVES)), dim3(DC_THREADS), 0, st, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.nsplit <= 1) return e;
-  hipLaunchKernelGGL((decode_merge_kernel<D, T>), dim3((unsigned)p.Hq, (unsigned)p.B), dim3(D), 0, st, p);
+  if (e != hipSuccess) return e;
+  const int64_t rows = (int64_t)p.B * p.rows_per_batch;
+  hipLaunchKernelGGL((decode_merge_kernel<D, T>), dim3((unsigned)rows), dim3(DC_THREADS), 0, st, p);
   return hipGetLastError();
-}
-
-static int decode_chunk(int chunk) {
-  if (chunk <= 0) return DC_DEFAULT_CHUNK;
-  return ((chunk + DC_STEP - 1) / DC_STEP) * DC_STEP;
 }
 
 }  // namespace nq
 
 using namespace nq;
 
-extern "C" int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int D, int max_len, int chunk) {
-  if (B <= 0 || Hq <= 0 || D <= 0 || max_len <= 0) return 0;
-  const int c = decode_chunk(chunk);
-  const int64_t nsplit = (max_len + c - 1) / c;
-  if (nsplit <= 1) return 0;
-  return (int64_t)B * Hq * nsplit * (D + 2) * (int64_t)sizeof(float);
+extern "C" int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int max_len, int chunk) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv) return 0;
+  return dc_workspace(B, Hq, Hkv, D, max_len, chunk);
 }
 
 extern "C" int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const void* k_cache,
@@ -352,9 +550,13 @@ extern "C" int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const
       return nq_fail(NQ_ERR_INVALID, "cache strides must be multiples of 16 bytes");
   if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
-  const int c = decode_chunk(chunk);
-  const int64_t need = nq_attn_decode_workspace_bytes(B, Hq, D, max_len, c);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+  if (k_strides[2] < D || v_strides[2] < D)
+    return nq_fail(NQ_ERR_INVALID, "cache rows must not overlap (seq stride >= head_dim)");
+  // one (batch, kv head) slab of max_len rows is addressed with 32-bit byte offsets
+  if ((int64_t)max_len * k_strides[2] * esz > 0x7fffffff || (int64_t)max_len * v_strides[2] * esz > 0x7fffffff)
+    return nq_fail(NQ_ERR_UNSUPPORTED, "max_len x seq stride exceeds 2 GiB per (batch, kv head)");
+  const int64_t need = dc_workspace(B, Hq, Hkv, D, max_len, chunk);
+  if (workspace == nullptr || workspace_bytes < need)
     return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
                    (long long)workspace_bytes);
   DecodeParams p{};
@@ -365,13 +567,14 @@ extern "C" int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const
   p.qw = q_weight; p.eps = eps; p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
   p.q_pos = q_pos; p.q_pos0 = q_pos0;
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = Hq / Hkv; p.NG = (p.G + 15) / 16;
-  p.chunk = c;
   p.max_len = max_len;
-  p.nsplit = (max_len + c - 1) / c;
-  if (p.nsplit > 1) {
-    p.ws_o = reinterpret_cast<float*>(workspace);
-    p.ws_ml = p.ws_o + (int64_t)B * Hq * p.nsplit * D;
-  }
+  p.rows_per_batch = Hkv * p.NG;
+  p.span = dc_span(chunk);
+  const int64_t nw = dc_waves(B, Hkv, p.NG, max_len, chunk);
+  if (nw / DC_WAVES > 0x7fffffff) return nq_fail(NQ_ERR_INVALID, "chunk %d too small for these sizes", chunk);
+  p.nwaves = (int)nw;
+  p.ws_o = reinterpret_cast<float*>(workspace);
+  p.ws_ml = p.ws_o + (nw + (int64_t)B * p.rows_per_batch) * 16 * D;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

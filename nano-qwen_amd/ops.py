@@ -271,9 +271,9 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 # Decode
 # ---------------------------------------------------------------------------
 
-def decode_workspace_bytes(B: int, Hq: int, D: int, max_len: int, chunk: int = 0) -> int:
+def decode_workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_len: int, chunk: int = 0) -> int:
     """Workspace size attention_decode needs for these sizes."""
-    return int(_lib.load().nq_attn_decode_workspace_bytes(B, Hq, D, max_len, chunk))
+    return int(_lib.load().nq_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk))
 
 
 def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -310,7 +310,7 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     if out is None:
         out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
     dev = q.device
-    need = decode_workspace_bytes(B, Hq, D, max_len, chunk)
+    need = decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
