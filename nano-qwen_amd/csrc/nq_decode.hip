@@ -29,9 +29,10 @@
 //   it writes an fp32 partial (unnormalised O, running max m, sum l) to slot
 //   (wave + row) of the workspace: because ranges are contiguous and ordered,
 //   two (wave, row) pairs with the same sum cannot both occur, so at most
-//   waves + rows slots are used.  decode_merge_kernel recomputes which waves
-//   touched each row and combines their partials (and writes zeros for rows
-//   with no keys).
+//   waves + rows slots are used.  The waves holding a row's first and last
+//   step record their index for it; decode_merge_kernel reads the two and
+//   combines the partials in between (and writes zeros for rows with no
+//   keys).
 //
 // The cache is read exactly once: HBM-bound at 16 FLOP/byte for G = 16.
 
@@ -43,8 +44,8 @@ namespace nq {
 constexpr int DC_THREADS = 256;  // four independent waves
 constexpr int DC_WAVES = DC_THREADS / 64;
 constexpr int DC_STEP = 32;      // keys per wave step
-constexpr int DC_WG_PER_CU = 2;  // resident workgroups per CU for the persistent grid
-constexpr int DC_MAX_WAVES = 2048;  // persistent grid cap: 256 CUs x 2 workgroups x 4 waves
+constexpr int DC_WG_PER_CU = 1;  // resident workgroups per CU for the persistent grid
+constexpr int DC_MAX_WAVES = 1024;  // persistent grid cap: 256 CUs x 1 workgroup x 4 waves
 
 struct DecodeParams {
   const void* q;
@@ -58,6 +59,7 @@ struct DecodeParams {
   int64_t osb, osh;
   float* ws_o;   // (slots, 16, D) unnormalised partial outputs
   float* ws_ml;  // (slots, 16, 2) running max (log2 units) and sum
+  int32_t* ws_rw;  // (rows, 2) first and last wave that covered each row
   const float* qw;
   float eps;
   const float* cos_tab;
@@ -150,16 +152,6 @@ __device__ int64_t total_steps(const DecodeParams& p, int lane) {
   return wave_sum_i64(acc) * p.rows_per_batch;
 }
 
-// Steps before the first row of batch b.
-__device__ int64_t steps_before(const DecodeParams& p, int lane, int b) {
-  int64_t acc = 0;
-  for (int base = 0; base < b; base += 64) {
-    const int bb = base + lane;
-    if (bb < b) acc += batch_steps(p, bb);
-  }
-  return wave_sum_i64(acc) * p.rows_per_batch;
-}
-
 // The batch whose rows hold global step q (q < N), and the steps before it.
 __device__ void find_batch(const DecodeParams& p, int lane, int64_t q, int& b_out, int64_t& before) {
   int64_t run = 0;
@@ -194,11 +186,6 @@ __device__ __forceinline__ int64_t waves_used(const DecodeParams& p, int64_t N) 
 __device__ __forceinline__ int64_t wave_begin(const DecodeParams& p, int64_t N, int64_t We, int64_t w) {
   return p.span > 0 ? min(N, w * p.span) : w * N / We;
 }
-// The wave whose range holds global step s.
-__device__ __forceinline__ int64_t wave_of(const DecodeParams& p, int64_t N, int64_t We, int64_t s) {
-  return p.span > 0 ? s / p.span : ((s + 1) * We - 1) / N;
-}
-
 // ---------------------------------------------------------------- kernels
 template <int D, typename T, bool PIPE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(DC_THREADS, DC_THREADS), amdgpu_waves_per_eu(DC_WG_PER_CU)))
@@ -220,10 +207,22 @@ decode_stream_kernel(DecodeParams p) {
   const int64_t q0 = wave_begin(p, N, We, w), q1 = wave_begin(p, N, We, w + 1);
   if (q0 >= q1) return;
 
+  // lens of up to 64 batch rows kept in a register: no memory round trip at a
+  // row boundary
+  const bool lens_in_reg = p.B <= 64;
+  const int lens_lane = lens_in_reg && lane < p.B ? batch_len(p, lane) : 0;
+  auto len_of = [&](int bb) {
+    return lens_in_reg ? __builtin_amdgcn_readlane(lens_lane, bb) : uniform(batch_len(p, bb));
+  };
+  auto steps_of = [&](int bb) {
+    const int l = len_of(bb);
+    return l > 0 ? (l + DC_STEP - 1) / DC_STEP : 0;
+  };
+
   int b;
   int64_t before;
   find_batch(p, lane, q0, b, before);
-  int nb = uniform(batch_steps(p, b));
+  int nb = steps_of(b);
   int j = (int)((q0 - before) / nb);   // row within the batch
   int ls = (int)((q0 - before) % nb);  // first step within the row
 
@@ -249,7 +248,7 @@ decode_stream_kernel(DecodeParams p) {
 
   int64_t q = q0;
   while (true) {
-    const int len = uniform(batch_len(p, b));
+    const int len = len_of(b);
     const int kvh = j / p.NG, hg = j % p.NG;
     const int nseg = (int)min((int64_t)(nb - ls), q1 - q);
     const bool whole = ls == 0 && nseg == nb;
@@ -402,6 +401,10 @@ decode_stream_kernel(DecodeParams p) {
     l_i += shfl_xor_f(l_i, 16);
     l_i += shfl_xor_f(l_i, 32);
     const int64_t r = ((int64_t)b * p.Hkv + kvh) * p.NG + hg;
+    if (lane == 0) {
+      if (ls == 0) p.ws_rw[r * 2] = (int32_t)w;
+      if (ls + nseg == nb) p.ws_rw[r * 2 + 1] = (int32_t)w;
+    }
     if (whole) {
       if (hvalid) {
         T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (int64_t)(kvh * p.G + gh) * p.osh;
@@ -422,47 +425,60 @@ decode_stream_kernel(DecodeParams p) {
     ls = 0;
     if (++j == p.rows_per_batch) {
       j = 0;
-      do nb = uniform(batch_steps(p, ++b)); while (nb == 0 && b + 1 < p.B);  // q < N: a batch with keys follows
+      do nb = steps_of(++b); while (nb == 0 && b + 1 < p.B);  // q < N: a batch with keys follows
     }
   }
 }
 
 // One workgroup per row (batch, kv head, head group): combines the partials
 // of the waves that covered the row, or writes zeros for a row without keys.
+// Thread t owns head t / 16 of the group and DPT consecutive dims.
 template <int D, typename T>
 __global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p) {
-  const int lane = threadIdx.x & 63;
+  constexpr int DPT = D / 16;  // dims per thread (8 or 4)
   const int64_t r = blockIdx.x;
   const int b = (int)(r / p.rows_per_batch), j = (int)(r % p.rows_per_batch);
   const int kvh = j / p.NG, hg = j % p.NG;
-  const int nb = batch_steps(p, b);
-  T* obase = reinterpret_cast<T*>(p.o) + b * p.osb;
+  const int hq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * DPT;
+  const int gh = hg * 16 + hq;
+  const int nb = uniform(batch_steps(p, b));
+  T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (int64_t)(kvh * p.G + (gh < p.G ? gh : 0)) * p.osh + d0;
   if (nb == 0) {
-    for (int idx = threadIdx.x; idx < 16 * D; idx += DC_THREADS) {
-      const int gh = hg * 16 + idx / D;
-      if (gh < p.G) obase[(int64_t)(kvh * p.G + gh) * p.osh + idx % D] = static_cast<T>(0.f);
+    if (gh < p.G) {
+      if constexpr (DPT == 8) store8<T>(orow, floatx8{});
+      else store4<T>(orow, floatx4{});
     }
     return;
   }
-  const int64_t N = total_steps(p, lane);
-  const int64_t We = waves_used(p, N);
-  const int64_t first = steps_before(p, lane, b) + (int64_t)j * nb;
-  const int64_t wf = wave_of(p, N, We, first), wl = wave_of(p, N, We, first + nb - 1);
-  if (wf == wl) return;  // one wave covered the row and wrote it
-  for (int idx = threadIdx.x; idx < 16 * D; idx += DC_THREADS) {
-    const int hq = idx / D, d = idx % D;
-    const int gh = hg * 16 + hq;
-    if (gh >= p.G) continue;
-    float M = -INFINITY;
-    for (int64_t w = wf; w <= wl; ++w) M = fmaxf(M, p.ws_ml[((w + r) * 16 + hq) * 2]);
-    float wsum = 0.f, osum = 0.f;
-    for (int64_t w = wf; w <= wl; ++w) {
-      const int64_t slot = w + r;
-      const float sc = fast_exp2(p.ws_ml[(slot * 16 + hq) * 2] - M);
-      wsum += p.ws_ml[(slot * 16 + hq) * 2 + 1] * sc;
-      osum += p.ws_o[(slot * 16 + hq) * D + d] * sc;
+  const int64_t wf = uniform(p.ws_rw[r * 2]), wl = uniform(p.ws_rw[r * 2 + 1]);
+  if (wf == wl || gh >= p.G) return;  // one wave covered the row and wrote it
+  const float* ml = p.ws_ml + ((wf + r) * 16 + hq) * 2;
+  const float* po = p.ws_o + ((wf + r) * 16 + hq) * D + d0;
+  const int ns = (int)(wl - wf + 1);
+  float M = -INFINITY;
+  for (int i = 0; i < ns; ++i) M = fmaxf(M, ml[i * 32]);
+  float wsum = 0.f;
+  float acc[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) acc[e] = 0.f;
+#pragma unroll 4
+  for (int i = 0; i < ns; ++i) {
+    const floatx2 m_l = *reinterpret_cast<const floatx2*>(ml + i * 32);
+    const float sc = fast_exp2(m_l[0] - M);
+    wsum += m_l[1] * sc;
+#pragma unroll
+    for (int e = 0; e < DPT; e += 4) {
+      const floatx4 o4 = *reinterpret_cast<const floatx4*>(po + (int64_t)i * 16 * D + e);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[e + k] += o4[k] * sc;
     }
-    obase[(int64_t)(kvh * p.G + gh) * p.osh + d] = static_cast<T>(osum / wsum);
+  }
+  const float inv = 1.0f / wsum;
+  if constexpr (DPT == 8) {
+    store8<T>(orow, floatx8{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv,
+                            acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv});
+  } else {
+    store4<T>(orow, floatx4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv});
   }
 }
 
@@ -478,8 +494,9 @@ static int64_t dc_waves(int B, int Hkv, int NG, int max_len, int chunk) {
 
 static int64_t dc_workspace(int B, int Hq, int Hkv, int D, int max_len, int chunk) {
   const int NG = (Hq / Hkv + 15) / 16;
-  const int64_t slots = dc_waves(B, Hkv, NG, max_len, chunk) + (int64_t)B * Hkv * NG;
-  return slots * 16 * (D + 2) * (int64_t)sizeof(float);
+  const int64_t rows = (int64_t)B * Hkv * NG;
+  const int64_t slots = dc_waves(B, Hkv, NG, max_len, chunk) + rows;
+  return slots * 16 * (D + 2) * (int64_t)sizeof(float) + rows * 2 * (int64_t)sizeof(int32_t);
 }
 
 template <int D, typename T>
@@ -540,11 +557,12 @@ extern "C" int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const
   if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
   if (!q || !k_cache || !v_cache || !o || !q_strides || !k_strides || !v_strides || !o_strides)
     return nq_fail(NQ_ERR_INVALID, "q, caches, o and their strides are required");
-  if (!nq_aligned16(q) || !nq_aligned16(k_cache) || !nq_aligned16(v_cache))
-    return nq_fail(NQ_ERR_INVALID, "q and cache base pointers must be 16-byte aligned");
+  if (!nq_aligned16(q) || !nq_aligned16(k_cache) || !nq_aligned16(v_cache) || !nq_aligned16(o))
+    return nq_fail(NQ_ERR_INVALID, "q, o and cache base pointers must be 16-byte aligned");
   const int esz = nq_dtype_size(dtype);
   for (int i = 0; i < 2; ++i)
-    if ((q_strides[i] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "q strides must be multiples of 16 bytes");
+    if ((q_strides[i] * esz) % 16 || (o_strides[i] * esz) % 16)
+      return nq_fail(NQ_ERR_INVALID, "q and o strides must be multiples of 16 bytes");
   for (int i = 0; i < 3; ++i)
     if ((k_strides[i] * esz) % 16 || (v_strides[i] * esz) % 16)
       return nq_fail(NQ_ERR_INVALID, "cache strides must be multiples of 16 bytes");
@@ -575,6 +593,7 @@ extern "C" int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const
   p.nwaves = (int)nw;
   p.ws_o = reinterpret_cast<float*>(workspace);
   p.ws_ml = p.ws_o + (nw + (int64_t)B * p.rows_per_batch) * 16 * D;
+  p.ws_rw = reinterpret_cast<int32_t*>(p.ws_ml + (nw + (int64_t)B * p.rows_per_batch) * 16 * 2);
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

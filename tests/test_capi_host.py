@@ -50,15 +50,16 @@ def test_argument_errors_need_no_gpu():
                                  1, 8, 2, 8, 4, 128, 0, None, 1e-6, None, None, 0,
                                  None, None, 0, 1, 0.0, None)
     assert rc == _lib.NQ_ERR_INVALID and b"S <= T" in lib.nq_last_error()
-    # slots = waves + rows; a slot holds 16 heads x (D outputs + max + sum) in fp32
+    # slots = waves + rows; a slot holds 16 heads x (D outputs + max + sum) in
+    # fp32, and each row records its first and last covering wave (2 x int32)
     slot = 16 * 130 * 4
-    assert lib.nq_attn_decode_workspace_bytes(64, 64, 4, 128, 32768, 0) == (2048 + 64 * 4) * slot
+    assert lib.nq_attn_decode_workspace_bytes(64, 64, 4, 128, 32768, 0) == (1024 + 256) * slot + 256 * 8
     # chunk 1024 = 32 steps per wave over 64 x 4 rows of 1024 steps
-    assert lib.nq_attn_decode_workspace_bytes(64, 64, 4, 128, 32768, 1024) == (8192 + 256) * slot
+    assert lib.nq_attn_decode_workspace_bytes(64, 64, 4, 128, 32768, 1024) == (8192 + 256) * slot + 256 * 8
     # G = 4 -> one head group per kv head; 4 rows x 32 steps / 32 = 4 waves
-    assert lib.nq_attn_decode_workspace_bytes(2, 8, 2, 128, 1000, 1024) == (4 + 4) * slot
+    assert lib.nq_attn_decode_workspace_bytes(2, 8, 2, 128, 1000, 1024) == (4 + 4) * slot + 4 * 8
     # G = 32 -> two head groups per kv head
-    assert lib.nq_attn_decode_workspace_bytes(1, 32, 1, 128, 64, 32) == (4 + 2) * slot
+    assert lib.nq_attn_decode_workspace_bytes(1, 32, 1, 128, 64, 32) == (4 + 2) * slot + 2 * 8
     assert lib.nq_attn_decode_workspace_bytes(2, 8, 3, 128, 1000, 0) == 0
     rc = lib.nq_attn_decode_fwd(None, None, None, st, None, st, None, None, None, None, 0,
                                 2, 8, 2, 128, 5000, 1024, 0, None, 1e-6, None, None, 0,
