@@ -99,7 +99,7 @@ int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
  * causal: query i sees key j iff j <= i + (T - S) (top-left == bottom-right
  *   when S == T, which is SDPA's is_causal in the reference).
  * sm_scale <= 0 selects 1/sqrt(D), SDPA's default (attention.py:110).
- * Requires 128 % (Hq / Hkv) == 0 and S <= T when causal.
+ * Requires 256 % (Hq / Hkv) == 0 and S <= T when causal.
  */
 int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides,

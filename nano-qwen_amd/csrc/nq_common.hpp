@@ -95,6 +95,41 @@ __device__ __forceinline__ bf16x8 lds_read_tr8(const bf16* p_lo, const bf16* p_h
   return __builtin_bit_cast(bf16x8, ab);
 }
 
+// The same transpose read issued as inline asm.  The compiler treats the
+// builtin as an LDS access it cannot tell apart from pending HBM->LDS loads
+// (global_load_lds) and puts s_waitcnt vmcnt(0) in front of it; a caller that
+// knows the tile it reads has landed uses this form and waits for the result
+// itself with lgkm_wait (the compiler does not track these reads).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char*)(p)));
+}
+template <int OFF>
+__device__ __forceinline__ shortx4 lds_read_tr4_nowait(uint32_t addr) {
+  shortx4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
+// rows r0..r0+3 at addr and r0+4..r0+7 at addr + HI bytes, as one operand
+template <int HI>
+__device__ __forceinline__ bf16x8 lds_read_tr8_nowait(uint32_t addr) {
+  shortx4 a = lds_read_tr4_nowait<0>(addr);
+  shortx4 b = lds_read_tr4_nowait<HI>(addr);
+  typedef short shortx8 __attribute__((ext_vector_type(8)));
+  shortx8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, ab);
+}
+// s_waitcnt lgkmcnt(N) (gfx9 encoding: vmcnt and expcnt left at their
+// maximum), fenced so that nothing is scheduled across it.  Valid when every
+// LDS access still outstanding is younger than the reads being waited for.
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
 // global_load_lds_dwordx4: lane t copies 16 bytes from its global address to
@@ -135,6 +170,18 @@ __device__ __forceinline__ void store4<float>(float* p, floatx4 v) {
 
 // ---------------------------------------------------------------- lanes
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// max / sum of lanes l and l^32 with v_permlane32_swap (a VALU op; __shfl_xor
+// goes through the LDS crossbar).  swap(x, x) leaves (x[l], x[l+32]) in lanes
+// l < 32 and (x[l-32], x[l]) in lanes l >= 32.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -5,12 +5,17 @@
 // fused into the Q load.
 //
 // Work decomposition
-//   A workgroup (4 waves, 256 lanes) owns 128 query rows that all read the
-//   same kv head: the G = Hq/Hkv query heads of one GQA group times
-//   BM = 128/G consecutive positions.  Every K/V tile it stages in LDS is
-//   therefore used by all G heads (the repeat_interleave of
-//   attention.py:106-108 never materialises).  All 128 rows share one causal
-//   frontier, so the whole workgroup walks the same key range.
+//   A workgroup of NW waves owns 32*NW query rows that all read the same kv
+//   head: the G = Hq/Hkv query heads of one GQA group times BM = 32*NW/G
+//   consecutive positions.  Every K/V tile it stages in LDS is therefore used
+//   by all G heads (the repeat_interleave of attention.py:106-108 never
+//   materialises).  All rows share one causal frontier, so the whole
+//   workgroup walks the same key range.  NW = 8 (256 rows, one workgroup per
+//   CU) halves the HBM/L2 -> LDS bytes per FLOP and the load instructions per
+//   wave against NW = 4 (each one stalls its wave for tens of clocks while the
+//   CU's load path, about 64 bytes per clock, drains); launches that would
+//   have fewer than PF_WIDE_MIN_WGS such workgroups use NW = 4 (two per CU),
+//   whose smaller causal q-blocks balance the tail better.
 //
 // Per wave: 32 query rows.  Scores are computed transposed, S^T = K Q^T, with
 // v_mfma_f32_32x32x16_bf16 (A = K tile from LDS, B = Q from registers).  In
@@ -46,8 +51,10 @@
 
 namespace nq {
 
-constexpr int PF_THREADS = 256;
-constexpr int PF_ROWS = 128;  // query rows per workgroup
+// A workgroup has NW waves (8, or 4 for launches too small to fill the GPU
+// with 8-wave workgroups) and 32 query rows per wave.
+constexpr int PF_MAX_ROWS = 256;
+constexpr int64_t PF_WIDE_MIN_WGS = 2048;  // 8-wave workgroups needed to prefer them
 constexpr int PF_BN = 64;     // keys per tile
 constexpr float PF_RESCALE_LOG2 = 8.0f;
 
@@ -78,23 +85,23 @@ __device__ __forceinline__ int key_perm32(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
-template <int D>
+template <int D, int NW>
 struct PfTile {
   static constexpr int ROW_BYTES = D * 2;
   static constexpr int CPR = D / 8;                   // 16-byte chunks per row
   static constexpr int RPL = 256 / ROW_BYTES;         // rows per 256-byte bank line
   static constexpr int TILE_BYTES = PF_BN * ROW_BYTES;
-  static constexpr int LOADS = TILE_BYTES / 1024 / 4; // 1 KiB load instructions per wave
+  static constexpr int LOADS = TILE_BYTES / 1024 / NW; // 1 KiB load instructions per wave
   // physical chunk of logical chunk c in row r
   __device__ static int k_chunk(int r, int c) { return c ^ ((r / RPL) & (CPR - 1)); }
   __device__ static int v_chunk(int r, int c) { return c ^ (4 * ((r / RPL) & (D / 32 - 1))); }
 };
 
-template <int D, typename T, bool CAUSAL, bool FUSE_Q>
-__global__ void __attribute__((amdgpu_flat_work_group_size(PF_THREADS, PF_THREADS),
+template <int D, typename T, bool CAUSAL, bool FUSE_Q, int NW>
+__global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW),
                                amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(PrefillParams p) {
-  using Tl = PfTile<D>;
+  using Tl = PfTile<D, NW>;
   constexpr int NDB = D / 16;        // 16-wide d blocks (QK^T k-steps)
   constexpr int NDO = D / 32;        // 32-wide d blocks (output tiles)
   constexpr int TB = Tl::TILE_BYTES;
@@ -137,15 +144,15 @@ prefill_kernel(PrefillParams p) {
       reinterpret_cast<const unsigned char*>(reinterpret_cast<const bf16*>(p.v) + b * p.vsb + kvh * p.vsh);
   const int64_t krow_bytes = p.kss * 2, vrow_bytes = p.vss * 2;
 
-  // ---- tile loads: load instruction G (0 <= G < 4*LOADS) fills LDS bytes
-  // [G*1024, G*1024+1024) of the tile, lane t the 16 bytes at +16*t; wave w
-  // issues G = 4*m + w.  With that interleave a lane's row offset within its
-  // 4-row (8-row for D=64) group, and so its chunk swizzle, is the same for
-  // every m: the address is a wave-uniform base (tile, m) in SGPRs plus one
-  // loop-invariant 32-bit lane offset.  In a tile that runs past T the rows
+  // ---- tile loads: load instruction G (0 <= G < NW*LOADS) fills LDS
+  // bytes [G*1024, G*1024+1024) of the tile, lane t the 16 bytes at +16*t;
+  // wave w issues G = NW*m + w.  With that interleave a lane's row
+  // offset within its 16-row (D=128) or 8-row (D=64) swizzle period, and so
+  // its chunk swizzle, is the same for every m: the address is a wave-uniform
+  // base (tile, m) in SGPRs plus one loop-invariant 32-bit lane offset.  In a tile that runs past T the rows
   // are clamped to T-1 instead (their scores are masked, so P = 0 there).
   constexpr int RPI = 64 / Tl::CPR;  // rows per load instruction
-  const int row0 = wave * RPI + lane / Tl::CPR;  // row of instruction m: row0 + 4*RPI*m
+  const int row0 = wave * RPI + lane / Tl::CPR;  // row of instruction m: row0 + NW*RPI*m
   const int pc0 = lane % Tl::CPR;
   const uint32_t koff = (uint32_t)(row0 * krow_bytes) + Tl::k_chunk(row0, pc0) * 16;
   const uint32_t voff = (uint32_t)(row0 * vrow_bytes) + Tl::v_chunk(row0, pc0) * 16;
@@ -156,13 +163,13 @@ prefill_kernel(PrefillParams p) {
       const unsigned char* tb = base + (int64_t)tile * PF_BN * row_bytes;
 #pragma unroll
       for (int m = 0; m < Tl::LOADS; ++m)
-        global_load_lds16(tb + m * 4 * RPI * row_bytes + off, smem + lds_w + m * 4096);
+        global_load_lds16(tb + m * NW * RPI * row_bytes + off, smem + lds_w + m * NW * 1024);
     } else {
       const uint32_t chunk_off = off - (uint32_t)(row0 * row_bytes);
 #pragma unroll
       for (int m = 0; m < Tl::LOADS; ++m) {
-        const int key = min(tile * PF_BN + row0 + m * 4 * RPI, p.T - 1);
-        global_load_lds16(base + key * row_bytes + chunk_off, smem + lds_w + m * 4096);
+        const int key = min(tile * PF_BN + row0 + m * NW * RPI, p.T - 1);
+        global_load_lds16(base + key * row_bytes + chunk_off, smem + lds_w + m * NW * 1024);
       }
     }
   };
@@ -195,7 +202,7 @@ prefill_kernel(PrefillParams p) {
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int e = 0; e < 8; ++e) ss += xf[db][e] * xf[db][e];
-        ss += shfl_xor_f(ss, 32);
+        ss = xor32_sum(ss);
         const float r = rsqrtf(ss / (float)D + p.eps);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
@@ -272,11 +279,38 @@ prefill_kernel(PrefillParams p) {
   floatx16 sA[2], sB[2];
   qk(0, sA[0], sA[1]);
 
-  // One 64-key tile.  Order inside a step: barrier + next loads; mask and row
-  // max of S[j] (branches); then one branch-free block in which the MFMAs of
-  // S[j+1] = K[j+1] Q^T are interleaved with the exp/sum/convert of P[j]
-  // (sched_group_barrier keeps them interleaved, since a wave issues in
-  // order); then O += V[j]^T P[j].
+  // masking of tile n0: keys past T, and (causal) keys past this row's frontier
+  auto mask_tile = [&](floatx16* s, int n0) {
+    if ((n0 + PF_BN > p.T) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff)) {
+      const int lim = CAUSAL ? min(p.T - 1, qi + coff) : p.T - 1;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = n0 + kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
+          if (key > lim) s[kb][i] = -INFINITY;
+        }
+    }
+  };
+  // row max of the current tile in log2 units (tile 0 holds key 0 for every
+  // row, so it is finite there; later tiles compare against a finite m_i)
+  float mx_cur;
+  {
+    mask_tile(sA, 0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(sA[kb][i], sA[kb][i + 1]));
+    mx_cur = xor32_max(mx) * p.scale_log2;
+  }
+
+  // One 64-key tile.  Order inside a step: barrier + next loads; rescale
+  // against the row max of S[j] (found in the previous step); then one
+  // branch-free block in which the MFMAs of S[j+1] = K[j+1] Q^T are
+  // interleaved with the exp/sum/convert of P[j] (sched_barrier keeps them
+  // interleaved, since a wave issues in order); then O += V[j]^T P[j] with the
+  // masking and row max of S[j+1] interleaved into those MFMAs.
   auto step = [&](auto parity, auto has_next, int j) {
     constexpr int P = decltype(parity)::value;       // == j & 1
     constexpr bool NEXT = decltype(has_next)::value;  // j + 1 < ntiles
@@ -292,28 +326,10 @@ prefill_kernel(PrefillParams p) {
       load_v(j + 1, P ^ 1);
     }
 
-    // masking: keys past T, and (causal) keys past this row's frontier
-    const bool need_mask = (n0 + PF_BN > p.T) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff);
-    if (need_mask) {
-      const int lim = CAUSAL ? min(p.T - 1, qi + coff) : p.T - 1;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = n0 + kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
-          if (key > lim) s_cur[kb][i] = -INFINITY;
-        }
-    }
-
     // online softmax (log2 domain); each lane owns one query row
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[kb][i]);
-    mx = fmaxf(mx, shfl_xor_f(mx, 32)) * p.scale_log2;
-    if (wave_any(mx > m_i + PF_RESCALE_LOG2)) {
-      const float m_new = fmaxf(m_i, mx);
+    (void)n0;
+    if (wave_any(mx_cur > m_i + PF_RESCALE_LOG2)) {
+      const float m_new = fmaxf(m_i, mx_cur);
       const float alpha = fast_exp2(m_i - m_new);  // 0 on the first tile
       l_i *= alpha;
 #pragma unroll
@@ -366,21 +382,41 @@ prefill_kernel(PrefillParams p) {
     }
     l_i += (acc[0] + acc[1]) + (acc[2] + acc[3]);
 
-    // Phase C: O^T += V[j]^T P^T, next transpose-read operand prefetched
-    const unsigned char* Vt = smem + (2 + P) * TB;
+    // Phase C: O^T += V[j]^T P^T, next transpose-read operand prefetched.
+    // V[j] landed before this step's barrier; the reads are issued as inline
+    // asm so the loads just issued for K[j+2] / V[j+1] keep flying through
+    // this phase (the builtin would wait for them).  No other LDS access is
+    // outstanding here, so lgkmcnt(2) means "all but the two newest reads".
+    const uint32_t Vt = lds_addr(smem + (2 + P) * TB);
     auto vread = [&](int idx) {
-      const bf16* src = reinterpret_cast<const bf16*>(Vt + v_off[idx % NDO] + (idx / NDO) * 16 * Tl::ROW_BYTES);
-      return lds_read_tr8(src, src + 4 * D);
+      return lds_read_tr8_nowait<8 * D>(Vt + v_off[idx % NDO] + (idx / NDO) * 16 * Tl::ROW_BYTES);
     };
+    if (NEXT) mask_tile(s_next, n0 + PF_BN);  // diagonal / last tiles only
+    constexpr int NPV = 4 * NDO;        // PV MFMAs
+    constexpr int MPER = 32 / NPV;      // S[j+1] elements folded into the max per MFMA
+    float mxn = -INFINITY;
     bf16x8 va = vread(0);
 #pragma unroll
-    for (int idx = 0; idx < 4 * NDO; ++idx) {
+    for (int idx = 0; idx < NPV; ++idx) {
       bf16x8 vn;
-      if (idx + 1 < 4 * NDO) vn = vread(idx + 1);
+      if (idx + 1 < NPV) {
+        vn = vread(idx + 1);
+        lgkm_wait<2>();
+      } else {
+        lgkm_wait<0>();
+      }
       oacc[idx % NDO] = mfma32(va, pop[idx / NDO], oacc[idx % NDO]);
+      if (NEXT) {
+#pragma unroll
+        for (int u = 0; u < MPER; ++u) {
+          const int e = idx * MPER + u;
+          mxn = fmaxf(mxn, s_next[e / 16][e % 16]);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
       va = vn;
     }
+    if (NEXT) mx_cur = xor32_max(mxn) * p.scale_log2;
   };
 
   using I0 = std::integral_constant<int, 0>;
@@ -399,7 +435,7 @@ prefill_kernel(PrefillParams p) {
     step(I0{}, No{}, j);
   }
 
-  l_i += shfl_xor_f(l_i, 32);
+  l_i = xor32_sum(l_i);
   if (!qvalid) return;
   const float inv_l = 1.f / l_i;
   T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + head * p.osh + (int64_t)qi * p.oss;
@@ -414,18 +450,23 @@ prefill_kernel(PrefillParams p) {
   if (p.lse && hh == 0) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = (m_i + __log2f(l_i)) * kLn2;
 }
 
-template <int D, typename T>
-static hipError_t launch_prefill(const PrefillParams& p, bool causal, bool fuse, hipStream_t st) {
+template <int D, typename T, int NW>
+static hipError_t launch_prefill_nw(const PrefillParams& p, bool causal, bool fuse, hipStream_t st) {
   dim3 grid((unsigned)(p.nqb * p.B * p.Hkv));
-  dim3 block(PF_THREADS);
+  dim3 block(64 * NW);
   if (causal) {
-    if (fuse) hipLaunchKernelGGL((prefill_kernel<D, T, true, true>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((prefill_kernel<D, T, true, false>), grid, block, 0, st, p);
+    if (fuse) hipLaunchKernelGGL((prefill_kernel<D, T, true, true, NW>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((prefill_kernel<D, T, true, false, NW>), grid, block, 0, st, p);
   } else {
-    if (fuse) hipLaunchKernelGGL((prefill_kernel<D, T, false, true>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((prefill_kernel<D, T, false, false>), grid, block, 0, st, p);
+    if (fuse) hipLaunchKernelGGL((prefill_kernel<D, T, false, true, NW>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((prefill_kernel<D, T, false, false, NW>), grid, block, 0, st, p);
   }
   return hipGetLastError();
+}
+
+template <int D, typename T>
+static hipError_t launch_prefill(const PrefillParams& p, int nw, bool causal, bool fuse, hipStream_t st) {
+  return nw == 8 ? launch_prefill_nw<D, T, 8>(p, causal, fuse, st) : launch_prefill_nw<D, T, 4>(p, causal, fuse, st);
 }
 
 }  // namespace nq
@@ -447,7 +488,7 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d S=%d T=%d)", B, Hq, Hkv, S, T);
   if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
   const int G = Hq / Hkv;
-  if (PF_ROWS % G) return nq_fail(NQ_ERR_UNSUPPORTED, "GQA group size %d must divide 128", G);
+  if (PF_MAX_ROWS % G) return nq_fail(NQ_ERR_UNSUPPORTED, "GQA group size %d must divide %d", G, PF_MAX_ROWS);
   if (causal && S > T) return nq_fail(NQ_ERR_INVALID, "causal attention needs S <= T (S=%d T=%d)", S, T);
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides)
     return nq_fail(NQ_ERR_INVALID, "q, k, v, o and their strides are required");
@@ -475,7 +516,10 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   p.qw = q_weight; p.eps = eps; p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
   p.q_pos = q_pos; p.q_pos_base = q_pos_base; p.q_pos0 = q_pos0;
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
-  p.BM = PF_ROWS / G;
+  // 256 rows per workgroup when that still gives enough workgroups, else 128
+  const int64_t wide_wgs = (int64_t)B * Hkv * ((S + PF_MAX_ROWS / G - 1) / (PF_MAX_ROWS / G));
+  const int nw = (128 % G == 0 && wide_wgs < PF_WIDE_MIN_WGS) ? 4 : 8;
+  p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
@@ -483,8 +527,8 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NQ_DTYPE_BF16)
-    e = (D == 128) ? launch_prefill<128, bf16>(p, causal, fuse, st) : launch_prefill<64, bf16>(p, causal, fuse, st);
+    e = (D == 128) ? launch_prefill<128, bf16>(p, nw, causal, fuse, st) : launch_prefill<64, bf16>(p, nw, causal, fuse, st);
   else
-    e = (D == 128) ? launch_prefill<128, float>(p, causal, fuse, st) : launch_prefill<64, float>(p, causal, fuse, st);
+    e = (D == 128) ? launch_prefill<128, float>(p, nw, causal, fuse, st) : launch_prefill<64, float>(p, nw, causal, fuse, st);
   return nq_check_launch(e);
 }

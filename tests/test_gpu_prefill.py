@@ -188,3 +188,19 @@ def test_long_context_yarn_full_size():
     for kvh in (0, 3):
         for (r0, r1), ref in zip(rows, _sampled_blocks(q, k, v, qw, kw, cos, sin, 0, kvh, G, rows)):
             assert_bf16_close(o[:, kvh * G:(kvh + 1) * G, r0:r1], ref, f"yarn kvh={kvh} rows={r0}")
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,B,S", [(64, 16, 16, 16, 2048), (128, 128, 8, 2, 4096)])
+def test_wide_workgroups(D, Hq, Hkv, B, S):
+    """Launches with at least 2048 workgroups of 256 rows run the 8-wave kernel
+    (D=64 with G=1, D=128 with G=16); oracle on sampled 128-row blocks."""
+    say(f"prefill 8-wave workgroups D={D} G={Hq // Hkv}")
+    G = Hq // Hkv
+    q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=1010 + D)
+    cos, sin = rope_tables(D, S, 1e6)
+    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                      cos.to(DEV), sin.to(DEV)).cpu()
+    rows = [(0, 128), (S // 2 + 40, S // 2 + 168), (S - 128, S)]
+    for b, kvh in ((0, 0), (B - 1, Hkv - 1)):
+        for (r0, r1), ref in zip(rows, _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows)):
+            assert_bf16_close(o[b:b + 1, kvh * G:(kvh + 1) * G, r0:r1], ref, f"wide b={b} kvh={kvh} rows={r0}")
