@@ -6,8 +6,8 @@ A step is one pass of the attention hot path over one batch of synthetic,
 seeded inputs already resident in HBM:
   prefill  K-Norm + RoPE row kernel (K-hat), then the fused prefill kernel
            (Q-Norm + RoPE on load, causal GQA FlashAttention forward);
-  decode   append of the new token's K-hat/V into the cache, then the split-K
-           decode kernel (+ its merge) over ragged lengths.
+  decode   append of the new token's K-hat/V into the cache, then the decode
+           kernel (a persistent grid streaming the ragged cache) and its merge.
 The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 (B8 S2048 Hq16 Hkv8 D128 causal bf16); FLOPs are the algorithmic
 4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
@@ -150,7 +150,7 @@ class Decode:
         ach = self.work / (kernel_ms * 1e-3) / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic,
-                "kernel": "decode_split_kernel + decode_merge_kernel", "kernel_ms": round(kernel_ms, 5)}
+                "kernel": "decode_stream_kernel + decode_merge_kernel", "kernel_ms": round(kernel_ms, 5)}
 
     def throughput(self, step_ms):
         return self.work / (step_ms * 1e-3) / 1e9, "GB/s"
@@ -170,7 +170,7 @@ def measured_traffic():
         if len(f) != 6 or line.startswith("#") or f[0] == "kernel":
             continue
         kern, w, fetch_mb, write_mb = f[0], f[1], float(f[4]), float(f[5])
-        if kern in ("prefill_kernel", "decode_split_kernel", "decode_merge_kernel"):
+        if kern in ("prefill_kernel", "decode_stream_kernel", "decode_merge_kernel"):
             out[w] = out.get(w, 0.0) + (fetch_mb + write_mb) * 1e6
     return {w: int(b) for w, b in out.items()}
 
