@@ -144,6 +144,14 @@ __device__ __forceinline__ void global_load_lds16(const void* g, void* lds) {
 // s_waitcnt vmcnt(0): all of this wave's vector-memory loads (including
 // global_load_lds) have completed.
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x3f70); }
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector-memory
+// instructions have completed (loads complete in order).  gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt and lgkmcnt left at their maximum.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
 
 template <typename T>
 __device__ __forceinline__ void store8(T* p, floatx8 v);

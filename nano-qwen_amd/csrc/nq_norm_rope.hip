@@ -9,11 +9,14 @@
 //
 // One launch processes up to three jobs (Q, K, V); V rows are copied (and
 // converted) without arithmetic.  Layout: a row is D contiguous elements;
-// (b, h, s) strides are free.  A row of D elements is handled by D/8 lanes,
-// each owning 8 consecutive elements (one 16-byte bf16 load).  The norm's
-// sum of squares is reduced across those lanes with xor shuffles; the RoPE
-// partner of element d (d + D/2) lives in the lane D/16 positions away.
-// HBM-bound: one read and one write per element, table reads hit L2.
+// (b, h, s) strides are free.  A row is handled by D/16 lanes: lane s of the
+// row owns elements [8s, 8s+8) and their RoPE partners [D/2+8s, D/2+8s+8)
+// (two 16-byte bf16 loads), so the rotation needs no cross-lane traffic; the
+// norm's sum of squares is reduced over the row's lanes with DPP adds
+// (row_half_mirror, then quad swaps), all VALU.  The grid is capped at 4
+// blocks per CU and loops over rows; in large launches each thread takes two
+// rows per step so that four row loads are in flight.  HBM-bound: one read and
+// one write per element; the weight and table reads hit the caches.
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
@@ -47,66 +50,99 @@ struct RowParams {
   int row0;
 };
 
-template <typename TI, typename TO, int D>
+// Sum over the row's lanes (LPR = 4 or 8 consecutive lanes) with DPP.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  if (LPR == 8) {  // lane i <- lane 7-i within each group of 8
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  }
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad xor 1
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad xor 2
+  return v;
+}
+
+constexpr int ROW_MAX_BLOCKS = 1024;  // grid cap: 4 blocks per CU on 256 CUs, looping over rows
+constexpr int64_t ROW_UNROLL_MIN = 32768;  // rows per job from which each thread takes two
+
+template <typename TI, typename TO, int D, int ROW_UNROLL>
 __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
-  constexpr int LPR = D / 8;          // lanes per row
+  constexpr int LPR = D / 16;         // lanes per row
   constexpr int RPW = 64 / LPR;       // rows per wave
-  constexpr int RPB = RPW * 4;        // rows per 256-thread block
+  constexpr int RPB = RPW * 4;        // rows per 256-thread block and unroll step
+  static_assert(LPR == 4 || LPR == 8, "D must be 64 or 128");
   const RowJob& jb = p.job[blockIdx.y];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int sub = lane % LPR;         // 8-element chunk within the row
-  const int64_t row = (int64_t)blockIdx.x * RPB + wave * RPW + lane / LPR;
+  const int sub = lane % LPR;         // chunk pair: [8sub, 8sub+8) and [D/2 + 8sub, ...)
   const int64_t nrows = (int64_t)p.B * jb.H * p.S;
-  const bool active = row < nrows;
-  // row -> (b, h, s) with s fastest
-  const int64_t rr = active ? row : 0;
-  const int s = (int)(rr % p.S);
-  const int h = (int)((rr / p.S) % jb.H);
-  const int b = (int)(rr / ((int64_t)p.S * jb.H));
-
-  const TI* src = reinterpret_cast<const TI*>(jb.src) + b * jb.sb + h * jb.sh + s * jb.ss + sub * 8;
-  floatx8 x = active ? Vec8<TI>::load_f32(src) : floatx8{0, 0, 0, 0, 0, 0, 0, 0};
-
+  floatx8 w1, w2;
   if (jb.norm) {
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-#pragma unroll
-    for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
-    const float r = rsqrtf(ss / (float)D + p.eps);
-    floatx8 w = Vec8<float>::load_f32(jb.weight + sub * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = x[e] * r * w[e];
+    w1 = Vec8<float>::load_f32(jb.weight + sub * 8);
+    w2 = Vec8<float>::load_f32(jb.weight + D / 2 + sub * 8);
   }
-  if (jb.rope) {
-    const int pos = clamp_pos(row_position(p.pos, p.pos_base, p.pos0, b, s, p.S), p.max_pos);
-    const int half_lanes = LPR / 2;
-    const bool first = sub < half_lanes;
-    const int dd = (sub % half_lanes) * 8;
-    floatx8 c = Vec8<float>::load_f32(p.cos_tab + (int64_t)pos * (D / 2) + dd);
-    floatx8 sn = Vec8<float>::load_f32(p.sin_tab + (int64_t)pos * (D / 2) + dd);
-    floatx8 y;
+  for (int64_t row0 = (int64_t)blockIdx.x * RPB * ROW_UNROLL + wave * RPW + lane / LPR; row0 < nrows;
+       row0 += (int64_t)gridDim.x * RPB * ROW_UNROLL) {
+  int bb[ROW_UNROLL], ss_[ROW_UNROLL], hh[ROW_UNROLL];
+  bool act[ROW_UNROLL];
+  floatx8 x1[ROW_UNROLL], x2[ROW_UNROLL];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float partner = shfl_xor_f(x[e], half_lanes);
-      // first half: x1*c - x2*s ; second half: x2*c + x1*s
-      y[e] = first ? (x[e] * c[e] - partner * sn[e]) : (x[e] * c[e] + partner * sn[e]);
+  for (int u = 0; u < ROW_UNROLL; ++u) {
+    const int64_t row = row0 + u * RPB;
+    act[u] = row < nrows;
+    // row -> (b, h, s) with s fastest
+    const int64_t rr = act[u] ? row : 0;
+    ss_[u] = (int)(rr % p.S);
+    hh[u] = (int)((rr / p.S) % jb.H);
+    bb[u] = (int)(rr / ((int64_t)p.S * jb.H));
+    const TI* src = reinterpret_cast<const TI*>(jb.src) + bb[u] * jb.sb + hh[u] * jb.sh + ss_[u] * jb.ss + sub * 8;
+    x1[u] = act[u] ? Vec8<TI>::load_f32(src) : floatx8{};
+    x2[u] = act[u] ? Vec8<TI>::load_f32(src + D / 2) : floatx8{};
+  }
+#pragma unroll
+  for (int u = 0; u < ROW_UNROLL; ++u) {
+    if (jb.norm) {
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq += x1[u][e] * x1[u][e] + x2[u][e] * x2[u][e];
+      sq = row_sum<LPR>(sq);
+      const float r = rsqrtf(sq / (float)D + p.eps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x1[u][e] = x1[u][e] * r * w1[e];
+        x2[u][e] = x2[u][e] * r * w2[e];
+      }
     }
-    x = y;
+    if (jb.rope) {
+      const int pos = clamp_pos(row_position(p.pos, p.pos_base, p.pos0, bb[u], ss_[u], p.S), p.max_pos);
+      const floatx8 c = Vec8<float>::load_f32(p.cos_tab + (int64_t)pos * (D / 2) + sub * 8);
+      const floatx8 sn = Vec8<float>::load_f32(p.sin_tab + (int64_t)pos * (D / 2) + sub * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = x1[u][e], b = x2[u][e];
+        x1[u][e] = a * c[e] - b * sn[e];
+        x2[u][e] = b * c[e] + a * sn[e];
+      }
+    }
+    if (act[u]) {
+      const int s = ss_[u];
+      const int drow = jb.use_row_base ? ((p.row_base ? p.row_base[bb[u]] : p.row0) + s) : s;
+      TO* dst = reinterpret_cast<TO*>(jb.dst) + bb[u] * jb.db + hh[u] * jb.dh + (int64_t)drow * jb.ds + sub * 8;
+      store8<TO>(dst, x1[u]);
+      store8<TO>(dst + D / 2, x2[u]);
+    }
   }
-  if (!active) return;
-  const int drow = jb.use_row_base ? ((p.row_base ? p.row_base[b] : p.row0) + s) : s;
-  TO* dst = reinterpret_cast<TO*>(jb.dst) + b * jb.db + h * jb.dh + (int64_t)drow * jb.ds + sub * 8;
-  store8<TO>(dst, x);
+  }
 }
 
 template <typename TI, typename TO, int D>
 static hipError_t launch_rows(const RowParams& p, int max_h, hipStream_t st) {
-  constexpr int RPB = (64 / (D / 8)) * 4;
+  constexpr int RPB = (64 / (D / 16)) * 4;  // rows per block and row step
   const int64_t nrows = (int64_t)p.B * max_h * p.S;
-  dim3 grid((unsigned)((nrows + RPB - 1) / RPB), (unsigned)p.njobs);
-  hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D>), grid, dim3(256), 0, st, p);
+  const int u = nrows >= ROW_UNROLL_MIN ? 2 : 1;
+  const int64_t blocks = (nrows + RPB * u - 1) / (RPB * u);
+  dim3 grid((unsigned)(blocks < ROW_MAX_BLOCKS ? blocks : ROW_MAX_BLOCKS), (unsigned)p.njobs);
+  if (u == 2) hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 2>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 1>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
