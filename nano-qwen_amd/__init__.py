@@ -11,6 +11,11 @@ Public surface, mirroring the reference:
   RotaryEmbedding, apply_rotary_pos_emb   model/rope.py:78-161
   flash_attention, apply_rope  kernels/flash_attn.py:130, kernels/rope.py:99
   AttentionConfig              attention fields of model/config.py:14-83
+  Qwen3Model, TransformerBlock, ModelConfig   model/transformer.py:24-162 (dense)
+  TextGenerator                eval/generate.py:20-183
+
+Extension with no reference counterpart: ``generate_greedy_batch`` (ragged
+batched greedy decoding against per-row cache lengths).
 """
 
 from .config import AttentionConfig
@@ -19,9 +24,12 @@ from .ops import (apply_rope, attention_decode, attention_prefill, decode_worksp
 from .norm import RMSNorm
 from .rope import RotaryEmbedding, apply_rotary_pos_emb, build_tables
 from .attention import Attention, KVCache, stats
+from .model import ModelConfig, Qwen3Model, TransformerBlock
+from .generate import TextGenerator, generate_greedy_batch
 
 __all__ = [
     "Attention", "KVCache", "RMSNorm", "RotaryEmbedding", "AttentionConfig",
     "apply_rotary_pos_emb", "build_tables", "flash_attention", "apply_rope",
     "qk_norm_rope", "attention_prefill", "attention_decode", "decode_workspace_bytes", "stats",
+    "ModelConfig", "Qwen3Model", "TransformerBlock", "TextGenerator", "generate_greedy_batch",
 ]

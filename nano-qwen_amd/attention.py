@@ -53,6 +53,15 @@ class KVCache:
     the tensors the reference's KVCache holds.  Capacity grows by doubling
     when an update does not fit (one copy); pass ``max_seq_len`` to size it
     once.
+
+    Ragged caches (an extension for batched serving, not in the reference):
+    after a right-padded prefill, ``set_lengths(lens)`` records per-row
+    lengths (an int32 device tensor).  Each one-token ``Attention`` step then
+    appends row b's key at slot ``lens[b]``, rotates it at position
+    ``lens[b]`` (unless position_ids are given), attends keys
+    ``[0, lens[b] + 1)`` and advances ``lens`` on the device.  ``seq_len`` is
+    then the storage extent (the largest row); rows past a row's length hold
+    padding and are never read.
     """
 
     def __init__(self, max_seq_len: Optional[int] = None):
@@ -62,6 +71,7 @@ class KVCache:
         self._len = 0
         self.key: Optional[torch.Tensor] = None
         self.value: Optional[torch.Tensor] = None
+        self.lens: Optional[torch.Tensor] = None
 
     @property
     def seq_len(self) -> int:
@@ -104,8 +114,22 @@ class KVCache:
             self.key = self._k[:, :, :self._len]
             self.value = self._v[:, :, :self._len]
 
+    def set_lengths(self, lens: torch.Tensor) -> None:
+        """Make the cache ragged: row b holds ``lens[b]`` (<= seq_len) valid keys."""
+        if self._k is None:
+            raise ValueError("set_lengths needs a filled cache")
+        lens = lens.to(device=self._k.device, dtype=torch.int32).contiguous()
+        if lens.shape != (self._k.shape[0],):
+            raise ValueError(f"lens must have shape ({self._k.shape[0]},), got {tuple(lens.shape)}")
+        if int(lens.max()) > self._len or int(lens.min()) < 1:
+            raise ValueError(f"lens must lie in [1, seq_len={self._len}]")
+        self.lens = lens
+
     def update(self, key: torch.Tensor, value: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         """Append (B, Hkv, S, D) rows; returns all valid rows (attention.py:31-38)."""
+        if self.lens is not None:
+            raise NotImplementedError("update() appends one slot for all rows; a ragged cache "
+                                      "is advanced by Attention's kernel path only")
         B, H, S, D = key.shape
         self.reserve(B, H, self._len + S, D, key.dtype, key.device)
         self._k[:, :, self._len:self._len + S] = key
@@ -115,6 +139,7 @@ class KVCache:
 
     def reset(self) -> None:
         self._len = 0
+        self.lens = None
         self._refresh()
 
 
@@ -186,6 +211,8 @@ class Attention(nn.Module):
                                       position_ids=position_ids, pos_offset=pos_offset, causal=True)
             return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
 
+        if kv_cache.lens is not None:
+            return self._ragged_decode(q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps)
         kv_cache.reserve(B, Hkv, past + S, D, k.dtype, k.device)
         kc, vc = kv_cache.storage()
         ops.qk_norm_rope(k=k4, v=v4, k_out=kc, v_out=vc, k_weight=kw, eps=eps, cos=cos, sin=sin,
@@ -204,9 +231,30 @@ class Attention(nn.Module):
                                   causal=self.cache_prefill_causal)
         return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
 
+    def _ragged_decode(self, q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps):
+        """One token per row against a ragged cache (see ``KVCache``)."""
+        B, H, S, D = q4.shape
+        if S != 1:
+            raise NotImplementedError("a ragged cache takes one token per row per step")
+        Hkv = k4.shape[1]
+        kv_cache.reserve(B, Hkv, kv_cache.seq_len + 1, D, k4.dtype, k4.device)
+        kc, vc = kv_cache.storage()
+        row = kv_cache.lens
+        pos = {"position_ids": position_ids} if position_ids is not None else {"pos_base": row}
+        ops.qk_norm_rope(k=k4, v=v4, k_out=kc, v_out=vc, k_weight=kw, eps=eps, cos=cos, sin=sin,
+                         kv_row_base=row, **pos)
+        row.add_(1)  # stream-ordered after the append above
+        kv_cache.advance(1)
+        qp = position_ids.reshape(B, -1)[:, 0] if position_ids is not None else None
+        o = ops.attention_decode(q4, kc, vc, row, max_len=kv_cache.seq_len, q_weight=qw, eps=eps,
+                                 cos=cos, sin=sin, q_pos=qp, q_pos0=-1)
+        return self.o_proj(o.reshape(B, 1, H * D))
+
     # ------------------------------------------------------------- torch path
     def _torch_forward(self, q, k, v, position_ids, attention_mask, kv_cache):
         """The reference's own arithmetic (attention.py:91-118) for autograd / masks."""
+        if kv_cache is not None and kv_cache.lens is not None:
+            raise NotImplementedError("ragged caches run on the kernel path only (no mask, no autograd)")
         B, S, _ = q.shape
         H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
         q = q.view(B, S, H, D).transpose(1, 2)

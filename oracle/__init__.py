@@ -19,3 +19,9 @@ from .attention_oracle import (  # noqa: F401
     attention_module_forward,
     OracleKVCache,
 )
+from .model_oracle import (  # noqa: F401
+    swiglu,
+    model_forward,
+    greedy_reference_protocol,
+    greedy_full_recompute,
+)
