@@ -145,6 +145,65 @@ int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const void* k_ca
                        const float* cos_tab, const float* sin_tab, int max_pos,
                        const int32_t* q_pos, int q_pos0, float sm_scale, void* stream);
 
+/*
+ * Paged KV caches.  A pool of pages (pages, Hkv, page_size, D), described by
+ * strides {page, head, row}; row t of sequence b is row t % page_size of page
+ * block_table[b * bt_stride + t / page_size] (int32 page ids).  A dense
+ * (B, Hkv, T_cap, D) cache is the pool of B pages of T_cap rows with the
+ * block table {0, 1, ..., B-1} and bt_stride 1.
+ *
+ * The reference has no paged cache: these replace the dense per-layer
+ * KVCache (model/attention.py:24-46) for batched serving, with the same
+ * contents (post-norm post-RoPE K, raw V).
+ */
+
+/*
+ * Single-token decode against a paged cache, with the new token's K/V append
+ * fused in (model/attention.py:95-115 at S == 1, plus KVCache.update,
+ * attention.py:31-38, in one launch).
+ *
+ * Without k_new (NULL): as nq_attn_decode_fwd, over keys [0, lens[b]) read
+ *   through the block table; lens is required.
+ * With k_new/v_new ((B, Hkv, D), strides {batch, head}, the projection
+ *   output before QK-Norm / RoPE): the new key is normed with k_weight (NULL =
+ *   no norm) and rotated at the query's position, written with v_new to row
+ *   lens[b] of the cache (its page must be mapped), and attended together with
+ *   keys [0, lens[b]).  The query position is q_pos[b], else q_pos0, else
+ *   lens[b].  lens_out (may be NULL; must not alias lens) receives lens + 1.
+ *   Calls that overlap on one sequence race; a single call is race-free.
+ * max_len bounds the keys attended per sequence (the appended one included)
+ *   and sizes the workspace (nq_attn_decode_workspace_bytes); bt_stride must
+ *   hold ceil(max_len / page_size) pages.  page_size must be a multiple of 32.
+ */
+int nq_attn_decode_paged_fwd(const void* q, const int64_t* q_strides, const void* k_new,
+                             const int64_t* k_new_strides, const void* v_new,
+                             const int64_t* v_new_strides, const float* k_weight, void* k_pool,
+                             const int64_t* k_pool_strides, void* v_pool,
+                             const int64_t* v_pool_strides, const int32_t* block_table,
+                             int64_t bt_stride, int page_size, const int32_t* lens,
+                             int32_t* lens_out, void* o, const int64_t* o_strides, void* workspace,
+                             int64_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_len,
+                             int chunk, int dtype, const float* q_weight, float eps,
+                             const float* cos_tab, const float* sin_tab, int max_pos,
+                             const int32_t* q_pos, int q_pos0, float sm_scale, void* stream);
+
+/*
+ * Append S rows per sequence to a paged cache: K rows QK-Normed (k_weight,
+ * NULL = none) and rotated (cos_tab, NULL = none), V rows copied.  Token s of
+ * sequence b becomes row row_base[b] + s (row_base NULL: row0 + s) of that
+ * sequence.  Positions as in nq_qk_norm_rope (pos, pos_base, pos0).  k or v
+ * may be NULL to append only the other.  The paged form of the K/V jobs of
+ * nq_qk_norm_rope (model/attention.py:31-38 and :95-103).
+ */
+int nq_kv_append_paged(const void* k, const int64_t* k_strides, const void* v,
+                       const int64_t* v_strides, void* k_pool, const int64_t* k_pool_strides,
+                       void* v_pool, const int64_t* v_pool_strides, const int32_t* block_table,
+                       int64_t bt_stride, int page_size, int B, int S, int Hkv, int D,
+                       int dtype_in, int dtype_out, const float* k_weight, float eps,
+                       const float* cos_tab, const float* sin_tab, int max_pos,
+                       const int32_t* pos, const int32_t* pos_base, int pos0,
+                       const int32_t* row_base, int row0, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,16 +14,18 @@ Public surface, mirroring the reference:
   Qwen3Model, TransformerBlock, ModelConfig   model/transformer.py:24-162 (dense)
   TextGenerator                eval/generate.py:20-183
 
-Extension with no reference counterpart: ``generate_greedy_batch`` (ragged
-batched greedy decoding against per-row cache lengths).
+Extensions with no reference counterpart: ``generate_greedy_batch`` (ragged
+batched greedy decoding against per-row cache lengths), ``PagedKVCache``
+(block-table page pool), ``attention_decode_paged`` (decode with the new
+token's K/V append fused in) and ``kv_append_paged``.
 """
 
 from .config import AttentionConfig
-from .ops import (apply_rope, attention_decode, attention_prefill, decode_workspace_bytes,
-                  flash_attention, qk_norm_rope)
+from .ops import (apply_rope, attention_decode, attention_decode_paged, attention_prefill,
+                  decode_workspace_bytes, flash_attention, kv_append_paged, qk_norm_rope)
 from .norm import RMSNorm
 from .rope import RotaryEmbedding, apply_rotary_pos_emb, build_tables
-from .attention import Attention, KVCache, stats
+from .attention import Attention, KVCache, PagedKVCache, stats
 from .model import ModelConfig, Qwen3Model, TransformerBlock
 from .generate import TextGenerator, generate_greedy_batch
 
@@ -32,4 +34,5 @@ __all__ = [
     "apply_rotary_pos_emb", "build_tables", "flash_attention", "apply_rope",
     "qk_norm_rope", "attention_prefill", "attention_decode", "decode_workspace_bytes", "stats",
     "ModelConfig", "Qwen3Model", "TransformerBlock", "TextGenerator", "generate_greedy_batch",
+    "PagedKVCache", "attention_decode_paged", "kv_append_paged",
 ]

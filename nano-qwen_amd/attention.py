@@ -72,6 +72,8 @@ class KVCache:
         self.key: Optional[torch.Tensor] = None
         self.value: Optional[torch.Tensor] = None
         self.lens: Optional[torch.Tensor] = None
+        self._lens_spare: Optional[torch.Tensor] = None
+        self._ident: Optional[torch.Tensor] = None
 
     @property
     def seq_len(self) -> int:
@@ -124,6 +126,22 @@ class KVCache:
         if int(lens.max()) > self._len or int(lens.min()) < 1:
             raise ValueError(f"lens must lie in [1, seq_len={self._len}]")
         self.lens = lens
+        self._lens_spare = None
+
+    def _spare_lens(self) -> torch.Tensor:
+        """The second lengths buffer: a fused decode step writes lens + 1 into it."""
+        if getattr(self, "_lens_spare", None) is None:
+            self._lens_spare = torch.empty_like(self.lens)
+        return self._lens_spare
+
+    def _identity_table(self) -> torch.Tensor:
+        """Block table [[0], [1], ...]: row b of the storage is page b."""
+        B = self._k.shape[0]
+        t = getattr(self, "_ident", None)
+        if t is None or t.shape[0] != B or t.device != self._k.device:
+            t = torch.arange(B, dtype=torch.int32, device=self._k.device).view(B, 1)
+            self._ident = t
+        return t
 
     def update(self, key: torch.Tensor, value: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         """Append (B, Hkv, S, D) rows; returns all valid rows (attention.py:31-38)."""
@@ -140,7 +158,135 @@ class KVCache:
     def reset(self) -> None:
         self._len = 0
         self.lens = None
+        self._lens_spare = None
         self._refresh()
+
+
+class PagedKVCache:
+    """KV cache held in fixed-size pages of a pool, addressed through a block table.
+
+    An extension for batched serving with no counterpart in the reference
+    (whose KVCache, model/attention.py:24-46, is one dense tensor per layer):
+    K-hat and V of sequence b, row t, live in page ``block_table[b, t //
+    page_size]`` at row ``t % page_size`` of the pools ``k_pool`` /
+    ``v_pool`` of shape (num_pages, Hkv, page_size, D).  Pages are taken from
+    a free list as sequences grow and returned by ``free`` / ``reset``, so
+    sequences of very different lengths share one pool without padding to
+    the longest.  ``page_size`` is a multiple of 32.
+
+    Semantics are the causal ones with true positions: a multi-token forward
+    appends its rows after each sequence's current length (causal attention
+    over the cache), and a one-token forward appends, rotates at and attends
+    up to each sequence's own length in one launch.  ``lens`` holds the
+    per-sequence lengths on the device; ``host_lens`` mirrors them (every
+    step adds a known number of rows), so page allocation never reads the
+    device.  ``set_lengths`` trims right-padded prompts after a batched
+    prefill, as ``KVCache.set_lengths`` does.
+    """
+
+    def __init__(self, num_pages: int, page_size: int = 64, max_pages_per_seq: Optional[int] = None):
+        if page_size <= 0 or page_size % 32:
+            raise ValueError(f"page_size must be a positive multiple of 32, got {page_size}")
+        if num_pages <= 0:
+            raise ValueError("num_pages must be positive")
+        self.num_pages = num_pages
+        self.page_size = page_size
+        self.max_pages_per_seq = max_pages_per_seq or num_pages
+        self.k_pool: Optional[torch.Tensor] = None
+        self.v_pool: Optional[torch.Tensor] = None
+        self.block_table: Optional[torch.Tensor] = None
+        self.lens: Optional[torch.Tensor] = None
+        self._lens_spare: Optional[torch.Tensor] = None
+        self.host_lens: list = []
+        self._pages: list = []
+        self._free = list(range(num_pages - 1, -1, -1))
+
+    # -- sizes
+    @property
+    def seq_len(self) -> int:
+        """Longest sequence held (the reference KVCache's seq_len for B = 1)."""
+        return max(self.host_lens, default=0)
+
+    @property
+    def free_pages(self) -> int:
+        return len(self._free)
+
+    def _setup(self, B: int, H: int, D: int, dtype, device) -> None:
+        if self.k_pool is None:
+            shape = (self.num_pages, H, self.page_size, D)
+            self.k_pool = torch.empty(shape, dtype=dtype, device=device)
+            self.v_pool = torch.empty(shape, dtype=dtype, device=device)
+        elif (self.k_pool.shape[1], self.k_pool.shape[3]) != (H, D) or self.k_pool.dtype != dtype:
+            raise ValueError(f"pool holds {tuple(self.k_pool.shape)} {self.k_pool.dtype}, "
+                             f"rows have Hkv={H} D={D} {dtype}")
+        if self.block_table is None:
+            self.block_table = torch.zeros(B, self.max_pages_per_seq, dtype=torch.int32, device=device)
+            self.lens = torch.zeros(B, dtype=torch.int32, device=device)
+            self.host_lens = [0] * B
+            self._pages = [[] for _ in range(B)]
+        elif self.block_table.shape[0] != B:
+            raise ValueError(f"cache holds {self.block_table.shape[0]} sequences, the batch has {B}")
+
+    def _grow(self, new_lens) -> None:
+        """Map pages so that sequence b can hold new_lens[b] rows."""
+        changed = False
+        for b, n in enumerate(new_lens):
+            need = -(-n // self.page_size)
+            if need > self.max_pages_per_seq:
+                raise ValueError(f"sequence {b} needs {need} pages, max_pages_per_seq is {self.max_pages_per_seq}")
+            while len(self._pages[b]) < need:
+                if not self._free:
+                    raise RuntimeError("PagedKVCache is out of pages")
+                self._pages[b].append(self._free.pop())
+                changed = True
+        if changed:
+            host = torch.zeros(self.block_table.shape, dtype=torch.int32)
+            for b, pages in enumerate(self._pages):
+                if pages:
+                    host[b, :len(pages)] = torch.tensor(pages, dtype=torch.int32)
+            self.block_table.copy_(host, non_blocking=False)
+
+    def _spare_lens(self) -> torch.Tensor:
+        if self._lens_spare is None:
+            self._lens_spare = torch.empty_like(self.lens)
+        return self._lens_spare
+
+    def set_lengths(self, lens) -> None:
+        """Trim each sequence to lens[b] rows (<= its current length); freed tail pages return to the pool."""
+        if self.lens is None:
+            raise ValueError("set_lengths needs a filled cache")
+        vals = [int(x) for x in (lens.tolist() if torch.is_tensor(lens) else lens)]
+        if len(vals) != len(self.host_lens):
+            raise ValueError(f"lens must have {len(self.host_lens)} entries")
+        for b, n in enumerate(vals):
+            if not 0 <= n <= self.host_lens[b]:
+                raise ValueError(f"lens[{b}] = {n} outside [0, {self.host_lens[b]}]")
+        for b, n in enumerate(vals):
+            keep = -(-n // self.page_size)
+            while len(self._pages[b]) > keep:
+                self._free.append(self._pages[b].pop())
+        self.host_lens = vals
+        self.lens.copy_(torch.tensor(vals, dtype=torch.int32))
+
+    def free(self, b: int) -> None:
+        """Drop sequence b (its pages return to the pool; its length becomes 0)."""
+        self.set_lengths([0 if i == b else n for i, n in enumerate(self.host_lens)])
+
+    def reset(self) -> None:
+        self._free = list(range(self.num_pages - 1, -1, -1))
+        self.block_table = None
+        self.lens = None
+        self._lens_spare = None
+        self.host_lens = []
+        self._pages = []
+
+    def gather(self, b: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Sequence b's K-hat and V as dense (Hkv, lens[b], D) tensors (a device copy)."""
+        n = self.host_lens[b]
+        pages = torch.tensor(self._pages[b], dtype=torch.long, device=self.k_pool.device)
+        k = self.k_pool.index_select(0, pages).transpose(0, 1).reshape(self.k_pool.shape[1], -1, self.k_pool.shape[3])
+        v = self.v_pool.index_select(0, pages).transpose(0, 1).reshape(self.v_pool.shape[1], -1, self.v_pool.shape[3])
+        return k[:, :n], v[:, :n]
 
 
 class Attention(nn.Module):
@@ -200,6 +346,8 @@ class Attention(nn.Module):
         qw = self.q_norm.weight if self.qk_norm else None
         kw = self.k_norm.weight if self.qk_norm else None
         eps = self.config.rms_norm_eps
+        if isinstance(kv_cache, PagedKVCache):
+            return self._paged_forward(q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps)
         past = kv_cache.seq_len if kv_cache is not None else 0
         pos_offset = past if (self.rope_positions == "cache" and position_ids is None) else 0
 
@@ -239,22 +387,66 @@ class Attention(nn.Module):
         Hkv = k4.shape[1]
         kv_cache.reserve(B, Hkv, kv_cache.seq_len + 1, D, k4.dtype, k4.device)
         kc, vc = kv_cache.storage()
-        row = kv_cache.lens
-        pos = {"position_ids": position_ids} if position_ids is not None else {"pos_base": row}
-        ops.qk_norm_rope(k=k4, v=v4, k_out=kc, v_out=vc, k_weight=kw, eps=eps, cos=cos, sin=sin,
-                         kv_row_base=row, **pos)
-        row.add_(1)  # stream-ordered after the append above
         kv_cache.advance(1)
+        # the dense storage is a pool of B pages of capacity rows each; one
+        # launch appends K-hat/V at row lens[b], attends lens[b] + 1 keys and
+        # writes lens + 1 into the spare lengths buffer
+        lens, lens_next = kv_cache.lens, kv_cache._spare_lens()
         qp = position_ids.reshape(B, -1)[:, 0] if position_ids is not None else None
-        o = ops.attention_decode(q4, kc, vc, row, max_len=kv_cache.seq_len, q_weight=qw, eps=eps,
-                                 cos=cos, sin=sin, q_pos=qp, q_pos0=-1)
+        o = ops.attention_decode_paged(q4, kc, vc, kv_cache._identity_table(), lens,
+                                       max_len=kv_cache.seq_len, k_new=k4, v_new=v4, k_weight=kw,
+                                       lens_out=lens_next, q_weight=qw, eps=eps, cos=cos, sin=sin,
+                                       q_pos=qp, q_pos0=-1)
+        kv_cache.lens = lens_next
+        kv_cache._lens_spare = lens
         return self.o_proj(o.reshape(B, 1, H * D))
+
+    def _paged_forward(self, q4, k4, v4, position_ids, cache, cos, sin, qw, kw, eps):
+        """Prefill into / decode against a PagedKVCache (causal, true positions)."""
+        B, H, S, D = q4.shape
+        Hkv = k4.shape[1]
+        cache._setup(B, Hkv, D, k4.dtype, k4.device)
+        past = list(cache.host_lens)
+        new = [n + S for n in past]
+        cache._grow(new)
+        if S == 1:
+            lens, lens_next = cache.lens, cache._spare_lens()
+            qp = position_ids.reshape(B, -1)[:, 0] if position_ids is not None else None
+            o = ops.attention_decode_paged(q4, cache.k_pool, cache.v_pool, cache.block_table, lens,
+                                           max_len=max(new), k_new=k4, v_new=v4, k_weight=kw,
+                                           lens_out=lens_next, q_weight=qw, eps=eps, cos=cos, sin=sin,
+                                           q_pos=qp, q_pos0=-1)
+            cache.lens, cache._lens_spare = lens_next, lens
+            cache.host_lens = new
+            return self.o_proj(o.reshape(B, 1, H * D))
+        if len(set(past)) != 1:
+            raise NotImplementedError("a multi-token forward into a PagedKVCache needs every sequence "
+                                      "at the same length")
+        p0 = past[0]
+        pos = {"position_ids": position_ids} if position_ids is not None else {"pos_offset": p0}
+        if p0 == 0:
+            k_hat = torch.empty(B, S, Hkv, D, dtype=k4.dtype, device=k4.device).transpose(1, 2)
+            ops.qk_norm_rope(k=k4, k_out=k_hat, k_weight=kw, eps=eps, cos=cos, sin=sin, **pos)
+            ops.kv_append_paged(k_hat, v4, cache.k_pool, cache.v_pool, cache.block_table)
+            k_all, v_all = k_hat, v4
+        else:
+            ops.kv_append_paged(k4, v4, cache.k_pool, cache.v_pool, cache.block_table, k_weight=kw,
+                                eps=eps, cos=cos, sin=sin, row_offset=p0, **pos)
+            T, P = p0 + S, cache.page_size
+            pages = cache.block_table[:, :-(-T // P)].long()
+            k_all = cache.k_pool[pages].permute(0, 2, 1, 3, 4).reshape(B, Hkv, -1, D)[:, :, :T]
+            v_all = cache.v_pool[pages].permute(0, 2, 1, 3, 4).reshape(B, Hkv, -1, D)[:, :, :T]
+        o = ops.attention_prefill(q4, k_all, v_all, q_weight=qw, eps=eps, cos=cos, sin=sin,
+                                  causal=True, **pos)
+        cache.lens.add_(S)
+        cache.host_lens = new
+        return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
 
     # ------------------------------------------------------------- torch path
     def _torch_forward(self, q, k, v, position_ids, attention_mask, kv_cache):
         """The reference's own arithmetic (attention.py:91-118) for autograd / masks."""
-        if kv_cache is not None and kv_cache.lens is not None:
-            raise NotImplementedError("ragged caches run on the kernel path only (no mask, no autograd)")
+        if isinstance(kv_cache, PagedKVCache) or (kv_cache is not None and kv_cache.lens is not None):
+            raise NotImplementedError("ragged and paged caches run on the kernel path only (no mask, no autograd)")
         B, S, _ = q.shape
         H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
         q = q.view(B, S, H, D).transpose(1, 2)

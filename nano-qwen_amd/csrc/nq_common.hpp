@@ -193,6 +193,63 @@ __device__ __forceinline__ float xor32_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Sum over groups of LPR = 4 or 8 consecutive lanes with DPP (all VALU).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(LPR == 4 || LPR == 8, "groups of 4 or 8 lanes");
+  if (LPR == 8) {  // lane i <- lane 7-i within each group of 8
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  }
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad xor 1
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad xor 2
+  return v;
+}
+
+// One head_dim row held by D/16 lanes: lane `sub` owns elements [8sub, 8sub+8)
+// (x1) and their rotate-half partners [D/2 + 8sub, D/2 + 8sub + 8) (x2).
+// RMSNorm with weight halves w1/w2 (when w1 is given), then RoPE with the
+// fp32 table row at `pos` (when cos_tab is given).  The same arithmetic, in
+// the same order, serves every kernel that writes a K-hat row.
+// The fused multiply-adds are written out so that every kernel that inlines
+// these rounds exactly alike (the compiler's own contraction may differ from
+// one context to the next).
+template <int D>
+__device__ __forceinline__ void norm_row(floatx8& x1, floatx8& x2, const floatx8& w1, const floatx8& w2,
+                                         float eps) {
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    sq = __builtin_fmaf(x1[e], x1[e], sq);
+    sq = __builtin_fmaf(x2[e], x2[e], sq);
+  }
+  sq = row_sum<D / 16>(sq);
+  const float r = rsqrtf(sq / (float)D + eps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x1[e] = x1[e] * r * w1[e];
+    x2[e] = x2[e] * r * w2[e];
+  }
+}
+__device__ __forceinline__ void rope_row(floatx8& x1, floatx8& x2, const floatx8& c, const floatx8& sn) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = x1[e], b = x2[e];
+    x1[e] = __builtin_fmaf(a, c[e], -(b * sn[e]));
+    x2[e] = __builtin_fmaf(b, c[e], a * sn[e]);
+  }
+}
+template <int D>
+__device__ __forceinline__ void norm_rope_row(floatx8& x1, floatx8& x2, const floatx8* w1, const floatx8* w2,
+                                              float eps, const float* cos_tab, const float* sin_tab, int pos,
+                                              int sub) {
+  if (w1) norm_row<D>(x1, x2, *w1, *w2, eps);
+  if (cos_tab) {
+    const floatx8 c = Vec8<float>::load_f32(cos_tab + (int64_t)pos * (D / 2) + sub * 8);
+    const floatx8 sn = Vec8<float>::load_f32(sin_tab + (int64_t)pos * (D / 2) + sub * 8);
+    rope_row(x1, x2, c, sn);
+  }
+}
+
 // Position of (b, s): explicit positions win, else base[b] + s, else pos0 + s.
 __device__ __forceinline__ int row_position(const int32_t* pos, const int32_t* pos_base, int pos0,
                                             int b, int s, int S) {

@@ -50,9 +50,11 @@ constexpr int DC_MAX_WAVES = 1024;  // persistent grid cap: 256 CUs x 1 workgrou
 struct DecodeParams {
   const void* q;
   int64_t qsb, qsh;
-  const void* kc;
+  // dense: (batch, kv head, row) strides of a (B, Hkv, T, D) cache;
+  // paged: (page, kv head, row) strides of a (pages, Hkv, page_size, D) pool
+  void* kc;
   int64_t ksb, ksh, kst;
-  const void* vc;
+  void* vc;
   int64_t vsb, vsh, vst;
   const int32_t* lens;
   void* o;
@@ -72,6 +74,20 @@ struct DecodeParams {
   int nwaves;          // waves launched
   int span;            // steps per wave; 0 = split N evenly over nwaves
   float scale_log2;
+  int append;          // 1: a new key per batch row is appended (see kn)
+  // paged: block table (row b at bt + b * bts) and rows per page (a multiple
+  // of DC_STEP)
+  const int32_t* bt;
+  int64_t bts;
+  int page;
+  // fused append: the new token's raw K (normed with kw, rotated) and V go to
+  // row lens[b] of the cache and are attended
+  const void* kn;
+  int64_t knsb, knsh;
+  const void* vn;
+  int64_t vnsb, vnsh;
+  const float* kw;
+  int32_t* lens_out;  // lens[b] + 1 after an append (never aliases lens)
 };
 
 // LDS tile of DC_STEP rows (keys) x D bf16, 16-byte chunks XOR-swizzled per row.
@@ -124,8 +140,9 @@ template <> struct Piece<float> {
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // ---------------------------------------------------------------- schedule
+// Keys attended by batch row b (the appended key included).
 __device__ __forceinline__ int batch_len(const DecodeParams& p, int b) {
-  return p.lens ? min(p.lens[b], p.max_len) : p.max_len;
+  return p.lens ? min(p.lens[b] + p.append, p.max_len) : p.max_len;
 }
 __device__ __forceinline__ int batch_steps(const DecodeParams& p, int b) {
   const int len = batch_len(p, b);
@@ -187,13 +204,14 @@ __device__ __forceinline__ int64_t wave_begin(const DecodeParams& p, int64_t N, 
   return p.span > 0 ? min(N, w * p.span) : w * N / We;
 }
 // ---------------------------------------------------------------- kernels
-template <int D, typename T, bool PIPE>
+template <int D, typename T, bool PIPE, bool PAGED, bool APPEND>
 __global__ void __attribute__((amdgpu_flat_work_group_size(DC_THREADS, DC_THREADS), amdgpu_waves_per_eu(DC_WG_PER_CU)))
 decode_stream_kernel(DecodeParams p) {
   using L = DcTile<D>;
   using P8 = Piece<T>;
   constexpr int NDQ = D / 32;  // 32-wide d blocks (QK^T k-steps)
   constexpr int NDO = D / 16;  // 16-wide d blocks (output tiles)
+  constexpr int LPR = D / 16;  // lanes holding one appended row
   __shared__ __attribute__((aligned(16))) unsigned char smem[DC_WAVES * 2 * L::BYTES];
 
   const int lane = threadIdx.x & 63;
@@ -255,7 +273,52 @@ decode_stream_kernel(DecodeParams p) {
     const int kbeg = ls * DC_STEP;
     const int kend = min(len, (ls + nseg) * DC_STEP);
 
-    // ---- query-side loads first (so waiting for them does not wait for K/V)
+    // ---- K/V of this (batch, kv head).  Keys [0, kend_ld) come from the
+    // cache; with an append, key len - 1 is the new one (built in registers),
+    // so its cache row is not read.  Keys past the range read as zeros.
+    const bool tail = APPEND && kend == len;  // this segment holds the appended key
+    const int kend_ld = tail ? kend - 1 : kend;
+    const int esz = (int)sizeof(T);
+    const T* kbase = reinterpret_cast<const T*>(p.kc) + kvh * p.ksh;
+    const T* vbase = reinterpret_cast<const T*>(p.vc) + kvh * p.vsh;
+    auto span_bytes = [&](int n, int64_t st) {
+      return n > 0 ? (uint32_t)(((int64_t)(n - 1) * st + D) * esz) : 0u;
+    };
+    __amdgpu_buffer_rsrc_t krs, vrs;
+    // paged: block-table entries [wbase, wbase + 64) of this row, one per lane;
+    // loaded before everything else so the first K/V loads wait on it alone
+    int wbase = 0, win = 0;
+    auto load_window = [&](int first) {
+      const int npg = (kend + p.page - 1) / p.page;
+      wbase = first;
+      win = first + lane < npg ? p.bt[b * p.bts + first + lane] : 0;
+    };
+    if constexpr (PAGED) {
+      load_window(kbeg / p.page);
+    } else {
+      krs = dc_buffer(kbase + b * p.ksb, span_bytes(kend_ld, p.kst));
+      vrs = dc_buffer(vbase + b * p.vsb, span_bytes(kend_ld, p.vst));
+    }
+
+    // ---- the appended row's operands, in the row layout of norm_row /
+    // rope_row: lane `sub` of each group of LPR lanes holds chunks sub and
+    // sub + D/16 of the row
+    const int sub = lane % LPR;
+    floatx8 ka1{}, ka2{}, va1{}, va2{}, kw1{}, kw2{}, kc1{}, ks1{};
+    if (tail) {
+      const T* ks = reinterpret_cast<const T*>(p.kn) + b * p.knsb + kvh * p.knsh + sub * 8;
+      const T* vs = reinterpret_cast<const T*>(p.vn) + b * p.vnsb + kvh * p.vnsh + sub * 8;
+      ka1 = Vec8<T>::load_f32(ks);
+      ka2 = Vec8<T>::load_f32(ks + D / 2);
+      va1 = Vec8<T>::load_f32(vs);
+      va2 = Vec8<T>::load_f32(vs + D / 2);
+      if (p.kw) {
+        kw1 = Vec8<float>::load_f32(p.kw + sub * 8);
+        kw2 = Vec8<float>::load_f32(p.kw + D / 2 + sub * 8);
+      }
+    }
+
+    // ---- query-side loads (before K/V, so waiting for them does not wait for K/V)
     const int gh = hg * 16 + c16;
     const bool hvalid = gh < p.G;
     const int head = kvh * p.G + (hvalid ? gh : 0);
@@ -267,8 +330,9 @@ decode_stream_kernel(DecodeParams p) {
 #pragma unroll
       for (int dq = 0; dq < NDQ; ++dq) wq[dq] = Vec8<float>::load_f32(p.qw + dq * 32 + grp * 8);
     }
+    const int pos =
+        p.cos_tab ? clamp_pos(p.q_pos ? uniform(p.q_pos[b]) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos) : 0;
     if (p.cos_tab) {
-      const int pos = clamp_pos(p.q_pos ? uniform(p.q_pos[b]) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos);
       const float* ct = p.cos_tab + (int64_t)pos * (D / 2);
       const float* st = p.sin_tab + (int64_t)pos * (D / 2);
 #pragma unroll
@@ -276,20 +340,32 @@ decode_stream_kernel(DecodeParams p) {
         cs[dq] = Vec8<float>::load_f32(ct + dq * 32 + grp * 8);
         sn[dq] = Vec8<float>::load_f32(st + dq * 32 + grp * 8);
       }
+      if (tail) {  // the appended key is rotated at the query's position
+        kc1 = Vec8<float>::load_f32(ct + sub * 8);
+        ks1 = Vec8<float>::load_f32(st + sub * 8);
+      }
     }
 
-    // ---- K/V of this (batch, kv head): keys [0, kend) are in range
-    const int esz = (int)sizeof(T);
-    const __amdgpu_buffer_rsrc_t krs = dc_buffer(reinterpret_cast<const T*>(p.kc) + b * p.ksb + kvh * p.ksh,
-                                                 (uint32_t)((int64_t)(kend - 1) * p.kst * esz + D * esz));
-    const __amdgpu_buffer_rsrc_t vrs = dc_buffer(reinterpret_cast<const T*>(p.vc) + b * p.vsb + kvh * p.vsh,
-                                                 (uint32_t)((int64_t)(kend - 1) * p.vst * esz + D * esz));
     const int kvo = (int)(lrow * p.kst * esz) + lc * 8 * esz;
     const int vvo = (int)(lrow * p.vst * esz) + lc * 8 * esz;
     const int kstep = (int)(L::RPI * p.kst * esz), vstep = (int)(L::RPI * p.vst * esz);
     typename P8::type kr[L::LOADS], vr[L::LOADS];
     auto load = [&](int k0) {
-      const int ks = (int)(k0 * p.kst * esz), vs = (int)(k0 * p.vst * esz);
+      int ks, vs;
+      if constexpr (PAGED) {
+        // a step never crosses a page: page_size is a multiple of DC_STEP
+        const int pg = k0 / p.page;
+        if (pg - wbase >= 64) load_window(pg);
+        const int64_t pid = __builtin_amdgcn_readlane(win, pg - wbase);
+        const int rel = k0 - pg * p.page;
+        const int nval = min(kend_ld, k0 + DC_STEP) - k0;
+        krs = dc_buffer(kbase + pid * p.ksb + (int64_t)rel * p.kst, span_bytes(nval, p.kst));
+        vrs = dc_buffer(vbase + pid * p.vsb + (int64_t)rel * p.vst, span_bytes(nval, p.vst));
+        ks = vs = 0;
+      } else {
+        ks = (int)(k0 * p.kst * esz);
+        vs = (int)(k0 * p.vst * esz);
+      }
 #pragma unroll
       for (int i = 0; i < L::LOADS; ++i) {
         kr[i] = P8::load(krs, kvo, ks + i * kstep);
@@ -297,6 +373,28 @@ decode_stream_kernel(DecodeParams p) {
       }
     };
     load(kbeg);
+
+    // ---- the appended key: QK-Norm, then RoPE (the arithmetic of the row
+    // kernel, so the cached row matches its K-hat bit for bit), written back
+    // by one wave per (batch, kv head); no wave of this launch reads that row
+    if (tail) {
+      if (p.kw) norm_row<D>(ka1, ka2, kw1, kw2, p.eps);
+      if (p.cos_tab) rope_row(ka1, ka2, kc1, ks1);
+      if (hg == 0 && lane < LPR) {
+        const int t = len - 1;
+        int64_t slab = b, row = t;
+        if constexpr (PAGED) {
+          slab = p.bt[b * p.bts + t / p.page];
+          row = t % p.page;
+        }
+        T* kd = reinterpret_cast<T*>(p.kc) + slab * p.ksb + kvh * p.ksh + row * p.kst + sub * 8;
+        T* vd = reinterpret_cast<T*>(p.vc) + slab * p.vsb + kvh * p.vsh + row * p.vst + sub * 8;
+        store8<T>(kd, ka1);
+        store8<T>(kd + D / 2, ka2);
+        store8<T>(vd, va1);
+        store8<T>(vd + D / 2, va2);
+      }
+    }
 
     // ---- Q operand (B of S^T = K Q^T): lane holds Q[head c16][dq*32 + grp*8 + e]
     bf16x8 qop[NDQ];
@@ -343,6 +441,15 @@ decode_stream_kernel(DecodeParams p) {
       for (int i = 0; i < L::LOADS; ++i) {
         *reinterpret_cast<bf16x8*>(kt + kwa[i]) = P8::to_bf16(kr[i]);
         *reinterpret_cast<bf16x8*>(vt + vwa[i]) = P8::to_bf16(vr[i]);
+      }
+      if (tail && s == nseg - 1 && lane < LPR) {
+        // the appended row replaces the zeros loaded for it
+        const int rr = len - 1 - k0;
+        const int c2 = sub + L::CPR / 2;
+        *reinterpret_cast<bf16x8*>(kt + rr * L::RB + ((sub ^ L::kswz(rr)) << 4)) = to_bf16x8(ka1);
+        *reinterpret_cast<bf16x8*>(kt + rr * L::RB + ((c2 ^ L::kswz(rr)) << 4)) = to_bf16x8(ka2);
+        *reinterpret_cast<bf16x8*>(vt + rr * L::RB + ((sub ^ L::vswz(rr)) << 4)) = to_bf16x8(va1);
+        *reinterpret_cast<bf16x8*>(vt + rr * L::RB + ((c2 ^ L::vswz(rr)) << 4)) = to_bf16x8(va2);
       }
       if (PIPE && s + 1 < nseg) load(k0 + DC_STEP);
 
@@ -441,6 +548,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p
   const int kvh = j / p.NG, hg = j % p.NG;
   const int hq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * DPT;
   const int gh = hg * 16 + hq;
+  if (p.lens_out && j == 0 && threadIdx.x == 0) p.lens_out[b] = p.lens[b] + 1;
   const int nb = uniform(batch_steps(p, b));
   T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (int64_t)(kvh * p.G + (gh < p.G ? gh : 0)) * p.osh + d0;
   if (nb == 0) {
@@ -499,12 +607,12 @@ static int64_t dc_workspace(int B, int Hq, int Hkv, int D, int max_len, int chun
   return slots * 16 * (D + 2) * (int64_t)sizeof(float) + rows * 2 * (int64_t)sizeof(int32_t);
 }
 
-template <int D, typename T>
+template <int D, typename T, bool PAGED, bool APPEND>
 static hipError_t launch_decode(DecodeParams p, hipStream_t st) {
-  auto kern = decode_stream_kernel<D, T, sizeof(T) == 2>;
+  auto kern = decode_stream_kernel<D, T, sizeof(T) == 2, PAGED, APPEND>;
   if (p.span == 0) {
     // persistent grid: as many waves as stay resident at once (<= DC_MAX_WAVES),
-    // worked out once per device
+    // worked out once per device and kernel variant
     static int resident[64];
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -531,6 +639,69 @@ static hipError_t launch_decode(DecodeParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Checks shared by both entry points, then the parameters that do not
+// depend on the cache layout.  Returns NQ_OK or the failure code.
+static int decode_setup(DecodeParams& p, const void* q, const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides, void* o, const int64_t* o_strides, void* workspace,
+                        int64_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_len, int chunk,
+                        int dtype, const float* q_weight, float eps, const float* cos_tab,
+                        const float* sin_tab, int max_pos, const int32_t* q_pos, int q_pos0, float sm_scale) {
+  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0)
+    return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d max_len=%d)", B, Hq, Hkv, max_len);
+  if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
+  if (!q || !o || !q_strides || !k_strides || !v_strides || !o_strides)
+    return nq_fail(NQ_ERR_INVALID, "q, caches, o and their strides are required");
+  if (!nq_aligned16(q) || !nq_aligned16(o))
+    return nq_fail(NQ_ERR_INVALID, "q, o and cache base pointers must be 16-byte aligned");
+  const int esz = nq_dtype_size(dtype);
+  for (int i = 0; i < 2; ++i)
+    if ((q_strides[i] * esz) % 16 || (o_strides[i] * esz) % 16)
+      return nq_fail(NQ_ERR_INVALID, "q and o strides must be multiples of 16 bytes");
+  for (int i = 0; i < 3; ++i)
+    if ((k_strides[i] * esz) % 16 || (v_strides[i] * esz) % 16)
+      return nq_fail(NQ_ERR_INVALID, "cache strides must be multiples of 16 bytes");
+  if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
+    return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
+  if (k_strides[2] < D || v_strides[2] < D)
+    return nq_fail(NQ_ERR_INVALID, "cache rows must not overlap (seq stride >= head_dim)");
+  const int64_t need = dc_workspace(B, Hq, Hkv, D, max_len, chunk);
+  if (workspace == nullptr || workspace_bytes < need)
+    return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
+                   (long long)workspace_bytes);
+  p.q = q; p.qsb = q_strides[0]; p.qsh = q_strides[1];
+  p.ksb = k_strides[0]; p.ksh = k_strides[1]; p.kst = k_strides[2];
+  p.vsb = v_strides[0]; p.vsh = v_strides[1]; p.vst = v_strides[2];
+  p.o = o; p.osb = o_strides[0]; p.osh = o_strides[1];
+  p.qw = q_weight; p.eps = eps; p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
+  p.q_pos = q_pos; p.q_pos0 = q_pos0;
+  p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = Hq / Hkv; p.NG = (p.G + 15) / 16;
+  p.max_len = max_len;
+  p.rows_per_batch = Hkv * p.NG;
+  p.span = dc_span(chunk);
+  const int64_t nw = dc_waves(B, Hkv, p.NG, max_len, chunk);
+  if (nw / DC_WAVES > 0x7fffffff) return nq_fail(NQ_ERR_INVALID, "chunk %d too small for these sizes", chunk);
+  p.nwaves = (int)nw;
+  p.ws_o = reinterpret_cast<float*>(workspace);
+  p.ws_ml = p.ws_o + (nw + (int64_t)B * p.rows_per_batch) * 16 * D;
+  p.ws_rw = reinterpret_cast<int32_t*>(p.ws_ml + (nw + (int64_t)B * p.rows_per_batch) * 16 * 2);
+  const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
+  p.scale_log2 = scale * kLog2e;
+  return NQ_OK;
+}
+
+template <bool PAGED, bool APPEND>
+static int decode_launch(const DecodeParams& p, int D, int dtype, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (dtype == NQ_DTYPE_BF16)
+    e = (D == 128) ? launch_decode<128, bf16, PAGED, APPEND>(p, st) : launch_decode<64, bf16, PAGED, APPEND>(p, st);
+  else
+    e = (D == 128) ? launch_decode<128, float, PAGED, APPEND>(p, st) : launch_decode<64, float, PAGED, APPEND>(p, st);
+  return nq_check_launch(e);
+}
+
 }  // namespace nq
 
 using namespace nq;
@@ -550,57 +721,75 @@ extern "C" int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const
                                   int max_pos, const int32_t* q_pos, int q_pos0, float sm_scale,
                                   void* stream) {
   nq_clear_error();
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
-  if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0)
-    return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d max_len=%d)", B, Hq, Hkv, max_len);
-  if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
-  if (!q || !k_cache || !v_cache || !o || !q_strides || !k_strides || !v_strides || !o_strides)
-    return nq_fail(NQ_ERR_INVALID, "q, caches, o and their strides are required");
-  if (!nq_aligned16(q) || !nq_aligned16(k_cache) || !nq_aligned16(v_cache) || !nq_aligned16(o))
+  DecodeParams p{};
+  int rc = decode_setup(p, q, q_strides, k_strides, v_strides, o, o_strides, workspace, workspace_bytes, B, Hq,
+                        Hkv, D, max_len, chunk, dtype, q_weight, eps, cos_tab, sin_tab, max_pos, q_pos, q_pos0,
+                        sm_scale);
+  if (rc != NQ_OK) return rc;
+  if (!k_cache || !v_cache) return nq_fail(NQ_ERR_INVALID, "q, caches, o and their strides are required");
+  if (!nq_aligned16(k_cache) || !nq_aligned16(v_cache))
     return nq_fail(NQ_ERR_INVALID, "q, o and cache base pointers must be 16-byte aligned");
-  const int esz = nq_dtype_size(dtype);
-  for (int i = 0; i < 2; ++i)
-    if ((q_strides[i] * esz) % 16 || (o_strides[i] * esz) % 16)
-      return nq_fail(NQ_ERR_INVALID, "q and o strides must be multiples of 16 bytes");
-  for (int i = 0; i < 3; ++i)
-    if ((k_strides[i] * esz) % 16 || (v_strides[i] * esz) % 16)
-      return nq_fail(NQ_ERR_INVALID, "cache strides must be multiples of 16 bytes");
-  if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
-    return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
-  if (k_strides[2] < D || v_strides[2] < D)
-    return nq_fail(NQ_ERR_INVALID, "cache rows must not overlap (seq stride >= head_dim)");
   // one (batch, kv head) slab of max_len rows is addressed with 32-bit byte offsets
+  const int esz = nq_dtype_size(dtype);
   if ((int64_t)max_len * k_strides[2] * esz > 0x7fffffff || (int64_t)max_len * v_strides[2] * esz > 0x7fffffff)
     return nq_fail(NQ_ERR_UNSUPPORTED, "max_len x seq stride exceeds 2 GiB per (batch, kv head)");
-  const int64_t need = dc_workspace(B, Hq, Hkv, D, max_len, chunk);
-  if (workspace == nullptr || workspace_bytes < need)
-    return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
-                   (long long)workspace_bytes);
+  p.kc = const_cast<void*>(k_cache);
+  p.vc = const_cast<void*>(v_cache);
+  p.lens = lens;
+  return decode_launch<false, false>(p, D, dtype, stream);
+}
+
+extern "C" int nq_attn_decode_paged_fwd(const void* q, const int64_t* q_strides, const void* k_new,
+                                        const int64_t* k_new_strides, const void* v_new,
+                                        const int64_t* v_new_strides, const float* k_weight,
+                                        void* k_pool, const int64_t* k_pool_strides, void* v_pool,
+                                        const int64_t* v_pool_strides, const int32_t* block_table,
+                                        int64_t bt_stride, int page_size, const int32_t* lens,
+                                        int32_t* lens_out, void* o, const int64_t* o_strides,
+                                        void* workspace, int64_t workspace_bytes, int B, int Hq,
+                                        int Hkv, int D, int max_len, int chunk, int dtype,
+                                        const float* q_weight, float eps, const float* cos_tab,
+                                        const float* sin_tab, int max_pos, const int32_t* q_pos,
+                                        int q_pos0, float sm_scale, void* stream) {
+  nq_clear_error();
   DecodeParams p{};
-  p.q = q; p.qsb = q_strides[0]; p.qsh = q_strides[1];
-  p.kc = k_cache; p.ksb = k_strides[0]; p.ksh = k_strides[1]; p.kst = k_strides[2];
-  p.vc = v_cache; p.vsb = v_strides[0]; p.vsh = v_strides[1]; p.vst = v_strides[2];
-  p.lens = lens; p.o = o; p.osb = o_strides[0]; p.osh = o_strides[1];
-  p.qw = q_weight; p.eps = eps; p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
-  p.q_pos = q_pos; p.q_pos0 = q_pos0;
-  p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = Hq / Hkv; p.NG = (p.G + 15) / 16;
-  p.max_len = max_len;
-  p.rows_per_batch = Hkv * p.NG;
-  p.span = dc_span(chunk);
-  const int64_t nw = dc_waves(B, Hkv, p.NG, max_len, chunk);
-  if (nw / DC_WAVES > 0x7fffffff) return nq_fail(NQ_ERR_INVALID, "chunk %d too small for these sizes", chunk);
-  p.nwaves = (int)nw;
-  p.ws_o = reinterpret_cast<float*>(workspace);
-  p.ws_ml = p.ws_o + (nw + (int64_t)B * p.rows_per_batch) * 16 * D;
-  p.ws_rw = reinterpret_cast<int32_t*>(p.ws_ml + (nw + (int64_t)B * p.rows_per_batch) * 16 * 2);
-  const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
-  p.scale_log2 = scale * kLog2e;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (dtype == NQ_DTYPE_BF16)
-    e = (D == 128) ? launch_decode<128, bf16>(p, st) : launch_decode<64, bf16>(p, st);
-  else
-    e = (D == 128) ? launch_decode<128, float>(p, st) : launch_decode<64, float>(p, st);
-  return nq_check_launch(e);
+  int rc = decode_setup(p, q, q_strides, k_pool_strides, v_pool_strides, o, o_strides, workspace,
+                        workspace_bytes, B, Hq, Hkv, D, max_len, chunk, dtype, q_weight, eps, cos_tab, sin_tab,
+                        max_pos, q_pos, q_pos0, sm_scale);
+  if (rc != NQ_OK) return rc;
+  if (!k_pool || !v_pool) return nq_fail(NQ_ERR_INVALID, "q, caches, o and their strides are required");
+  if (!nq_aligned16(k_pool) || !nq_aligned16(v_pool))
+    return nq_fail(NQ_ERR_INVALID, "q, o and cache base pointers must be 16-byte aligned");
+  if (!block_table || !lens) return nq_fail(NQ_ERR_INVALID, "a paged cache needs the block table and lens");
+  if (page_size <= 0 || page_size % DC_STEP)
+    return nq_fail(NQ_ERR_UNSUPPORTED, "page_size must be a positive multiple of %d, got %d", DC_STEP, page_size);
+  if (bt_stride < (max_len + page_size - 1) / page_size)
+    return nq_fail(NQ_ERR_INVALID, "bt_stride %lld holds fewer than the %d pages of max_len %d",
+                   (long long)bt_stride, (max_len + page_size - 1) / page_size, max_len);
+  if ((k_new == nullptr) != (v_new == nullptr))
+    return nq_fail(NQ_ERR_INVALID, "k_new and v_new go together");
+  const int esz = nq_dtype_size(dtype);
+  if (k_new) {
+    if (!k_new_strides || !v_new_strides)
+      return nq_fail(NQ_ERR_INVALID, "k_new and v_new need their strides");
+    if (!nq_aligned16(k_new) || !nq_aligned16(v_new))
+      return nq_fail(NQ_ERR_INVALID, "k_new and v_new must be 16-byte aligned");
+    for (int i = 0; i < 2; ++i)
+      if ((k_new_strides[i] * esz) % 16 || (v_new_strides[i] * esz) % 16)
+        return nq_fail(NQ_ERR_INVALID, "k_new and v_new strides must be multiples of 16 bytes");
+    if (lens_out == lens) return nq_fail(NQ_ERR_INVALID, "lens_out must not alias lens");
+  } else if (lens_out) {
+    return nq_fail(NQ_ERR_INVALID, "lens_out is written only with an append (k_new/v_new)");
+  }
+  p.kc = k_pool; p.vc = v_pool;
+  p.bt = block_table; p.bts = bt_stride; p.page = page_size;
+  p.lens = lens;
+  if (k_new) {
+    p.append = 1;
+    p.kn = k_new; p.knsb = k_new_strides[0]; p.knsh = k_new_strides[1];
+    p.vn = v_new; p.vnsb = v_new_strides[0]; p.vnsh = v_new_strides[1];
+    p.kw = k_weight;
+    p.lens_out = lens_out;
+  }
+  return p.append ? decode_launch<true, true>(p, D, dtype, stream) : decode_launch<true, false>(p, D, dtype, stream);
 }

@@ -48,18 +48,13 @@ struct RowParams {
   int pos0;
   const int32_t* row_base;
   int row0;
+  // paged destination for row-base jobs: row t of sequence b lands in page
+  // block_table[b * bt_stride + t / page_size], row t % page_size; the job's
+  // destination strides are then (page, head, row)
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int page_size;
 };
-
-// Sum over the row's lanes (LPR = 4 or 8 consecutive lanes) with DPP.
-template <int LPR>
-__device__ __forceinline__ float row_sum(float v) {
-  if (LPR == 8) {  // lane i <- lane 7-i within each group of 8
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
-  }
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad xor 1
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad xor 2
-  return v;
-}
 
 constexpr int ROW_MAX_BLOCKS = 1024;  // grid cap: 4 blocks per CU on 256 CUs, looping over rows
 constexpr int64_t ROW_UNROLL_MIN = 32768;  // rows per job from which each thread takes two
@@ -75,7 +70,7 @@ __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
   const int wave = threadIdx.x >> 6;
   const int sub = lane % LPR;         // chunk pair: [8sub, 8sub+8) and [D/2 + 8sub, ...)
   const int64_t nrows = (int64_t)p.B * jb.H * p.S;
-  floatx8 w1, w2;
+  floatx8 w1{}, w2{};
   if (jb.norm) {
     w1 = Vec8<float>::load_f32(jb.weight + sub * 8);
     w2 = Vec8<float>::load_f32(jb.weight + D / 2 + sub * 8);
@@ -100,33 +95,18 @@ __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
   }
 #pragma unroll
   for (int u = 0; u < ROW_UNROLL; ++u) {
-    if (jb.norm) {
-      float sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sq += x1[u][e] * x1[u][e] + x2[u][e] * x2[u][e];
-      sq = row_sum<LPR>(sq);
-      const float r = rsqrtf(sq / (float)D + p.eps);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x1[u][e] = x1[u][e] * r * w1[e];
-        x2[u][e] = x2[u][e] * r * w2[e];
-      }
-    }
-    if (jb.rope) {
-      const int pos = clamp_pos(row_position(p.pos, p.pos_base, p.pos0, bb[u], ss_[u], p.S), p.max_pos);
-      const floatx8 c = Vec8<float>::load_f32(p.cos_tab + (int64_t)pos * (D / 2) + sub * 8);
-      const floatx8 sn = Vec8<float>::load_f32(p.sin_tab + (int64_t)pos * (D / 2) + sub * 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a = x1[u][e], b = x2[u][e];
-        x1[u][e] = a * c[e] - b * sn[e];
-        x2[u][e] = b * c[e] + a * sn[e];
-      }
-    }
+    const int pos = jb.rope ? clamp_pos(row_position(p.pos, p.pos_base, p.pos0, bb[u], ss_[u], p.S), p.max_pos) : 0;
+    norm_rope_row<D>(x1[u], x2[u], jb.norm ? &w1 : nullptr, &w2, p.eps, jb.rope ? p.cos_tab : nullptr,
+                     p.sin_tab, pos, sub);
     if (act[u]) {
       const int s = ss_[u];
       const int drow = jb.use_row_base ? ((p.row_base ? p.row_base[bb[u]] : p.row0) + s) : s;
-      TO* dst = reinterpret_cast<TO*>(jb.dst) + bb[u] * jb.db + hh[u] * jb.dh + (int64_t)drow * jb.ds + sub * 8;
+      int64_t slab = bb[u], prow = drow;
+      if (jb.use_row_base && p.block_table) {
+        slab = p.block_table[bb[u] * p.bt_stride + drow / p.page_size];
+        prow = drow % p.page_size;
+      }
+      TO* dst = reinterpret_cast<TO*>(jb.dst) + slab * jb.db + hh[u] * jb.dh + prow * jb.ds + sub * 8;
       store8<TO>(dst, x1[u]);
       store8<TO>(dst + D / 2, x2[u]);
     }
@@ -150,17 +130,16 @@ static hipError_t launch_rows(const RowParams& p, int max_h, hipStream_t st) {
 
 using namespace nq;
 
-extern "C" int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
-                               const int64_t* q_out_strides, const void* k,
-                               const int64_t* k_strides, void* k_out,
-                               const int64_t* k_out_strides, const void* v,
-                               const int64_t* v_strides, void* v_out,
-                               const int64_t* v_out_strides, int B, int S, int Hq, int Hkv,
-                               int D, int dtype_in, int dtype_out, const float* q_weight,
-                               const float* k_weight, float eps, const float* cos_tab,
-                               const float* sin_tab, int max_pos, const int32_t* pos,
-                               const int32_t* pos_base, int pos0,
-                               const int32_t* kv_row_base, int kv_row0, void* stream) {
+static int qk_norm_rope_impl(const void* q, const int64_t* q_strides, void* q_out,
+                             const int64_t* q_out_strides, const void* k, const int64_t* k_strides,
+                             void* k_out, const int64_t* k_out_strides, const void* v,
+                             const int64_t* v_strides, void* v_out, const int64_t* v_out_strides,
+                             int B, int S, int Hq, int Hkv, int D, int dtype_in, int dtype_out,
+                             const float* q_weight, const float* k_weight, float eps,
+                             const float* cos_tab, const float* sin_tab, int max_pos,
+                             const int32_t* pos, const int32_t* pos_base, int pos0,
+                             const int32_t* kv_row_base, int kv_row0, const int32_t* block_table,
+                             int64_t bt_stride, int page_size, void* stream) {
   nq_clear_error();
   if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
   if (B <= 0 || S <= 0) return nq_fail(NQ_ERR_INVALID, "B and S must be positive (B=%d S=%d)", B, S);
@@ -171,6 +150,7 @@ extern "C" int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_
   const int esz_in = nq_dtype_size(dtype_in), esz_out = nq_dtype_size(dtype_out);
   RowParams p{};
   p.B = B; p.S = S; p.D = D; p.eps = eps;
+  p.block_table = block_table; p.bt_stride = bt_stride; p.page_size = page_size;
   p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
   p.pos = pos; p.pos_base = pos_base; p.pos0 = pos0;
   p.row_base = kv_row_base; p.row0 = kv_row0;
@@ -210,4 +190,44 @@ extern "C" int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_
   else NQ_ROWS(float, float);
 #undef NQ_ROWS
   return nq_check_launch(e);
+}
+
+extern "C" int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
+                               const int64_t* q_out_strides, const void* k,
+                               const int64_t* k_strides, void* k_out,
+                               const int64_t* k_out_strides, const void* v,
+                               const int64_t* v_strides, void* v_out,
+                               const int64_t* v_out_strides, int B, int S, int Hq, int Hkv,
+                               int D, int dtype_in, int dtype_out, const float* q_weight,
+                               const float* k_weight, float eps, const float* cos_tab,
+                               const float* sin_tab, int max_pos, const int32_t* pos,
+                               const int32_t* pos_base, int pos0,
+                               const int32_t* kv_row_base, int kv_row0, void* stream) {
+  return qk_norm_rope_impl(q, q_strides, q_out, q_out_strides, k, k_strides, k_out, k_out_strides, v,
+                           v_strides, v_out, v_out_strides, B, S, Hq, Hkv, D, dtype_in, dtype_out,
+                           q_weight, k_weight, eps, cos_tab, sin_tab, max_pos, pos, pos_base, pos0,
+                           kv_row_base, kv_row0, nullptr, 0, 0, stream);
+}
+
+extern "C" int nq_kv_append_paged(const void* k, const int64_t* k_strides, const void* v,
+                                  const int64_t* v_strides, void* k_pool,
+                                  const int64_t* k_pool_strides, void* v_pool,
+                                  const int64_t* v_pool_strides, const int32_t* block_table,
+                                  int64_t bt_stride, int page_size, int B, int S, int Hkv, int D,
+                                  int dtype_in, int dtype_out, const float* k_weight, float eps,
+                                  const float* cos_tab, const float* sin_tab, int max_pos,
+                                  const int32_t* pos, const int32_t* pos_base, int pos0,
+                                  const int32_t* row_base, int row0, void* stream) {
+  if (!block_table || page_size <= 0 || bt_stride <= 0) {
+    nq_clear_error();
+    return nq_fail(NQ_ERR_INVALID, "a block table, bt_stride > 0 and page_size > 0 are required");
+  }
+  if (!k && !v) {
+    nq_clear_error();
+    return nq_fail(NQ_ERR_INVALID, "nothing to append (k and v are both null)");
+  }
+  return qk_norm_rope_impl(nullptr, nullptr, nullptr, nullptr, k, k_strides, k_pool, k_pool_strides, v,
+                           v_strides, v_pool, v_pool_strides, B, S, 0, Hkv, D, dtype_in, dtype_out,
+                           nullptr, k_weight, eps, cos_tab, sin_tab, max_pos, pos, pos_base, pos0,
+                           row_base, row0, block_table, bt_stride, page_size, stream);
 }

@@ -24,7 +24,7 @@ from typing import Callable, List, Optional, Sequence, Tuple
 import torch
 import torch.nn.functional as F
 
-from .attention import KVCache
+from .attention import KVCache, PagedKVCache
 
 
 def _device_of(model) -> torch.device:
@@ -142,7 +142,7 @@ def _fixed_semantics(model):
 @torch.no_grad()
 def generate_greedy_batch(model, prompts: Sequence[Sequence[int]], max_new_tokens: int,
                           stop_tokens: Optional[Sequence[int]] = None,
-                          return_logits: bool = False
+                          return_logits: bool = False, page_size: Optional[int] = None
                           ) -> Tuple[List[List[int]], Optional[List[torch.Tensor]]]:
     """Greedy decoding of several prompts at once against a ragged KV cache.
 
@@ -150,10 +150,12 @@ def generate_greedy_batch(model, prompts: Sequence[Sequence[int]], max_new_token
     pass (row b's last real token sits at ``len_b - 1`` and never sees the
     padding); each cache is then made ragged with the true lengths, so every
     decode step appends row b's key at slot ``len_b + t``, rotates it at that
-    position and attends exactly its own keys.  A row stops at its first stop
-    token (not included) or after ``max_new_tokens``.  Returns the generated
-    tokens per row and, with ``return_logits``, the fp32 logits each token was
-    chosen from (one (n_b, vocab) tensor per row).
+    position and attends exactly its own keys.  With ``page_size`` the caches
+    are ``PagedKVCache`` page pools (the padding's pages are returned after
+    the prefill) instead of dense per-row buffers.  A row stops at its first
+    stop token (not included) or after ``max_new_tokens``.  Returns the
+    generated tokens per row and, with ``return_logits``, the fp32 logits each
+    token was chosen from (one (n_b, vocab) tensor per row).
     """
     if not prompts or any(len(p) == 0 for p in prompts):
         raise ValueError("every prompt needs at least one token")
@@ -166,7 +168,12 @@ def generate_greedy_batch(model, prompts: Sequence[Sequence[int]], max_new_token
         ids[b, :len(p)] = torch.as_tensor(list(p), dtype=torch.long)
     ids = ids.to(dev)
     stop = set(stop_tokens or [])
-    caches = [KVCache(max_seq_len=L + max_new_tokens) for _ in range(len(model.layers))]
+    if page_size is None:
+        caches = [KVCache(max_seq_len=L + max_new_tokens) for _ in range(len(model.layers))]
+    else:
+        per_seq = -(-(L + max_new_tokens) // page_size)
+        caches = [PagedKVCache(B * per_seq, page_size=page_size, max_pages_per_seq=per_seq)
+                  for _ in range(len(model.layers))]
     out: List[List[int]] = [[] for _ in range(B)]
     steps: List[List[torch.Tensor]] = [[] for _ in range(B)]
     done = [False] * B
@@ -177,7 +184,7 @@ def generate_greedy_batch(model, prompts: Sequence[Sequence[int]], max_new_token
         logits = logits[torch.arange(B, device=dev), last]
         lens_t = torch.as_tensor(lens, dtype=torch.int32, device=dev)
         for c in caches:
-            c.set_lengths(lens_t.clone())
+            c.set_lengths(lens_t.clone() if page_size is None else lens)
         for _ in range(max_new_tokens):
             nxt = logits.argmax(dim=-1)
             toks = nxt.tolist()

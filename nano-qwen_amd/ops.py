@@ -27,6 +27,8 @@ __all__ = [
     "qk_norm_rope",
     "attention_prefill",
     "attention_decode",
+    "attention_decode_paged",
+    "kv_append_paged",
     "decode_workspace_bytes",
     "flash_attention",
     "apply_rope",
@@ -329,6 +331,173 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
     call = KernelCall(_lib.load().nq_attn_decode_fwd, args, len(args) - 1, "nq_attn_decode_fwd",
                       (q, k_cache, v_cache, lens_t, workspace, cos_t, sin_t, qp, qw, q_str, o_str), out)
+    return call if plan else call.launch()
+
+
+# ---------------------------------------------------------------------------
+# Paged caches
+# ---------------------------------------------------------------------------
+
+def _pool_check(pool: torch.Tensor, name: str) -> None:
+    if pool.dim() != 4:
+        raise ValueError(f"{name} must be (pages, Hkv, page_size, D), got {tuple(pool.shape)}")
+    _rows_out(pool, name)
+
+
+def _block_table(bt: torch.Tensor, B: int, dev) -> torch.Tensor:
+    if bt.dim() != 2 or bt.shape[0] != B:
+        raise ValueError(f"block_table must be (B={B}, pages per sequence), got {tuple(bt.shape)}")
+    bt = _i32(bt, dev)
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    return bt
+
+
+def kv_append_paged(k: Optional[torch.Tensor], v: Optional[torch.Tensor], k_pool: torch.Tensor,
+                    v_pool: torch.Tensor, block_table: torch.Tensor, *,
+                    k_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                    cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                    position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
+                    pos_base: Optional[torch.Tensor] = None,
+                    row_offset: int = 0, row_base: Optional[torch.Tensor] = None,
+                    plan: bool = False):
+    """Write K-hat (QK-Norm + RoPE of k) and V rows into a paged pool.
+
+    k/v: (B, Hkv, S, D), any (b, h, s) strides; k_pool/v_pool:
+    (pages, Hkv, page_size, D).  Token s of sequence b is row
+    ``t = row_base[b] + s`` (else ``row_offset + s``) of that sequence and
+    lands in page ``block_table[b, t // page_size]``, row ``t % page_size``.
+    Positions as in ``qk_norm_rope``.  k_weight None skips the norm and
+    cos/sin None skip the rotation (a plain copy).
+    """
+    ref = k if k is not None else v
+    if ref is None:
+        raise ValueError("nothing to append")
+    _require_device(k, v, k_pool, v_pool, block_table)
+    dev = ref.device
+    B, Hkv, S, D = ref.shape
+    for name, pool in (("k_pool", k_pool), ("v_pool", v_pool)):
+        _pool_check(pool, name)
+        if pool.shape[1] != Hkv or pool.shape[3] != D:
+            raise ValueError(f"{name} holds Hkv={pool.shape[1]} D={pool.shape[3]}, rows have Hkv={Hkv} D={D}")
+    if k_pool.dtype != v_pool.dtype:
+        raise TypeError("k_pool and v_pool must share one dtype")
+    if k is not None and v is not None and k.dtype != v.dtype:
+        raise TypeError("k and v must share one dtype")
+    bt = _block_table(block_table, B, dev)
+    k = _rows_in(k) if k is not None else None
+    v = _rows_in(v) if v is not None else None
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    pos = _i32(position_ids, dev)
+    if pos is not None and tuple(pos.shape) != (B, S):
+        pos = pos.expand(B, S).contiguous()
+    pb = _i32(pos_base, dev)
+    rb = _i32(row_base, dev)
+    kw = _f32(k_weight, dev)
+    st = _lib.strides3
+    args = (
+        _ptr(k), st(k.stride()[:3]) if k is not None else None,
+        _ptr(v), st(v.stride()[:3]) if v is not None else None,
+        _ptr(k_pool), st(k_pool.stride()[:3]), _ptr(v_pool), st(v_pool.stride()[:3]),
+        _ptr(bt), bt.stride(0), k_pool.shape[2],
+        B, S, Hkv, D, _code(ref), _code(k_pool), _ptr(kw), float(eps),
+        _ptr(cos_t), _ptr(sin_t), max_pos, _ptr(pos), _ptr(pb), int(pos_offset),
+        _ptr(rb), int(row_offset), _stream(ref))
+    call = KernelCall(_lib.load().nq_kv_append_paged, args, len(args) - 1, "nq_kv_append_paged",
+                      (k, v, bt, cos_t, sin_t, pos, pb, rb, kw), (k_pool, v_pool))
+    return call if plan else call.launch()
+
+
+def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                           block_table: torch.Tensor, lens: torch.Tensor, *, max_len: int,
+                           k_new: Optional[torch.Tensor] = None, v_new: Optional[torch.Tensor] = None,
+                           k_weight: Optional[torch.Tensor] = None,
+                           lens_out: Optional[torch.Tensor] = None,
+                           q_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                           cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                           q_pos: Optional[torch.Tensor] = None, q_pos0: int = -1,
+                           sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                           workspace: Optional[torch.Tensor] = None, chunk: int = 0,
+                           plan: bool = False):
+    """Single-token GQA decode against a paged cache, with an optional fused append.
+
+    q: (B, Hq, D) or (B, Hq, 1, D) pre-norm query; k_pool/v_pool:
+    (pages, Hkv, page_size, D) with page_size a multiple of 32; row t of
+    sequence b is page ``block_table[b, t // page_size]``, row
+    ``t % page_size``.  A dense (B, Hkv, T_cap, D) cache is the pool of B
+    pages of T_cap rows with block_table ``[[0], [1], ...]``.
+
+    Without k_new: attends keys [0, lens[b]); the query is rotated at
+    q_pos[b], else q_pos0, else lens[b] - 1.  With k_new/v_new (B, Hkv, D) or
+    (B, Hkv, 1, D), the new token's K (normed with k_weight, rotated at the
+    query's position, which defaults to lens[b]) and V are written to row
+    lens[b] and attended together with keys [0, lens[b]); ``lens_out`` (not
+    aliasing lens) then receives lens + 1.  ``max_len`` bounds the keys
+    attended per sequence (the appended one included); the block table must
+    map every page up to it.  Returns (B, Hq, D).
+    """
+    _require_device(q, k_pool, v_pool, block_table, lens, k_new, v_new, lens_out, out)
+    if q.dim() == 4:
+        q = q[:, :, 0]
+    B, Hq, D = q.shape
+    for name, pool in (("k_pool", k_pool), ("v_pool", v_pool)):
+        _pool_check(pool, name)
+    if k_pool.shape != v_pool.shape or k_pool.shape[3] != D:
+        raise ValueError("pool shapes do not match q")
+    Hkv, page = k_pool.shape[1], k_pool.shape[2]
+    if q.dtype != k_pool.dtype or q.dtype != v_pool.dtype:
+        raise TypeError("q and the pools must share one dtype")
+    bt = _block_table(block_table, B, dev := q.device)
+    if not 0 < max_len <= bt.shape[1] * page:
+        raise ValueError(f"max_len must be in [1, {bt.shape[1] * page}] (block table columns x page_size)")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is not None:
+        if k_new.dim() == 4:
+            k_new, v_new = k_new[:, :, 0], v_new[:, :, 0]
+        if tuple(k_new.shape) != (B, Hkv, D) or tuple(v_new.shape) != (B, Hkv, D):
+            raise ValueError(f"k_new/v_new must be (B={B}, Hkv={Hkv}, D={D})")
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise TypeError("k_new/v_new must have q's dtype")
+        k_new, v_new = _rows_in(k_new), _rows_in(v_new)
+    elif lens_out is not None:
+        raise ValueError("lens_out is written only with an append (k_new/v_new)")
+    dt = _code(q)
+    q = _rows_in(q)
+    lens_t = _i32(lens, dev)
+    if lens_out is not None:
+        if lens_out.dtype != torch.int32 or not lens_out.is_contiguous() or lens_out.numel() != B:
+            raise ValueError("lens_out must be a contiguous int32 tensor of B elements")
+        if lens_out.data_ptr() == lens_t.data_ptr():
+            raise ValueError("lens_out must not alias lens")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q.dtype, device=dev)
+    need = decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk)
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    qp = _i32(q_pos, dev)
+    qw, kw = _f32(q_weight, dev), _f32(k_weight, dev)
+    q_str = (ctypes.c_int64 * 2)(q.stride(0), q.stride(1))
+    o_str = (ctypes.c_int64 * 2)(out.stride(0), out.stride(1))
+    kn_str = vn_str = None
+    if k_new is not None:
+        kn_str = (ctypes.c_int64 * 2)(k_new.stride(0), k_new.stride(1))
+        vn_str = (ctypes.c_int64 * 2)(v_new.stride(0), v_new.stride(1))
+    st = _lib.strides3
+    args = (
+        _ptr(q), q_str, _ptr(k_new), kn_str, _ptr(v_new), vn_str, _ptr(kw),
+        _ptr(k_pool), st(k_pool.stride()[:3]), _ptr(v_pool), st(v_pool.stride()[:3]),
+        _ptr(bt), bt.stride(0), page, _ptr(lens_t), _ptr(lens_out),
+        _ptr(out), o_str, _ptr(workspace), wbytes,
+        B, Hq, Hkv, D, int(max_len), int(chunk), dt, _ptr(qw), float(eps),
+        _ptr(cos_t), _ptr(sin_t), max_pos, _ptr(qp), int(q_pos0),
+        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    call = KernelCall(_lib.load().nq_attn_decode_paged_fwd, args, len(args) - 1,
+                      "nq_attn_decode_paged_fwd",
+                      (q, k_new, v_new, bt, lens_t, workspace, cos_t, sin_t, qp, qw, kw,
+                       q_str, o_str, kn_str, vn_str), out)
     return call if plan else call.launch()
 
 

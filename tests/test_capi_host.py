@@ -31,6 +31,11 @@ def test_library_loads_and_exports_every_header_symbol():
         assert hasattr(lib, name), name
     loaded = _lib.load()
     assert loaded.nq_version() == 100
+    # a call with no jobs succeeds without touching the GPU and clears the error text
+    st = _lib.strides3((0, 0, 0))
+    assert loaded.nq_qk_norm_rope(None, st, None, st, None, st, None, st, None, st, None, st,
+                                  1, 1, 1, 1, 128, 0, 0, None, None, 1e-6, None, None, 0,
+                                  None, None, 0, None, 0, None) == _lib.NQ_OK
     assert loaded.nq_last_error() == b""
 
 
