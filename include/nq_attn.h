@@ -204,6 +204,23 @@ int nq_kv_append_paged(const void* k, const int64_t* k_strides, const void* v,
                        const int32_t* pos, const int32_t* pos_base, int pos0,
                        const int32_t* row_base, int row0, void* stream);
 
+/*
+ * Merge an attention partial into an accumulator, both computed over disjoint
+ * key sets: the online-softmax combine of ring attention
+ * (distributed/context_parallel.py:120-127 and 133-134), done with each
+ * part's log-sum-exp.
+ *
+ * o / o_part: (B, H, S, D) normalised outputs with strides {batch, head, seq};
+ * lse / lse_part: fp32 (B, H, S) contiguous natural-log sum-exp of the scaled
+ *   scores (as nq_attn_prefill_fwd writes), -inf for a row with no keys.
+ * On return lse = log(exp(lse) + exp(lse_part)) and
+ *   o = o * exp(lse_old - lse) + o_part * exp(lse_part - lse); a row empty in
+ *   both stays empty (o = 0, lse = -inf).
+ */
+int nq_attn_merge(void* o, const int64_t* o_strides, float* lse, const void* o_part,
+                  const int64_t* part_strides, const float* lse_part, int B, int H, int S, int D,
+                  int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

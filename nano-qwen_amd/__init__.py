@@ -13,6 +13,7 @@ Public surface, mirroring the reference:
   AttentionConfig              attention fields of model/config.py:14-83
   Qwen3Model, TransformerBlock, ModelConfig   model/transformer.py:24-162 (dense)
   TextGenerator                eval/generate.py:20-183
+  RingAttention, split_sequence   distributed/context_parallel.py:17-140 (one GPU's share)
 
 Extensions with no reference counterpart: ``generate_greedy_batch`` (ragged
 batched greedy decoding against per-row cache lengths), ``PagedKVCache``
@@ -28,6 +29,8 @@ from .rope import RotaryEmbedding, apply_rotary_pos_emb, build_tables
 from .attention import Attention, KVCache, PagedKVCache, stats
 from .model import ModelConfig, Qwen3Model, TransformerBlock
 from .generate import TextGenerator, generate_greedy_batch
+from .ops import attention_merge_
+from .ring import RingAttention, ring_attention_all_ranks, ring_schedule, ring_step, split_sequence
 
 __all__ = [
     "Attention", "KVCache", "RMSNorm", "RotaryEmbedding", "AttentionConfig",
@@ -35,4 +38,6 @@ __all__ = [
     "qk_norm_rope", "attention_prefill", "attention_decode", "decode_workspace_bytes", "stats",
     "ModelConfig", "Qwen3Model", "TransformerBlock", "TextGenerator", "generate_greedy_batch",
     "PagedKVCache", "attention_decode_paged", "kv_append_paged",
+    "attention_merge_", "RingAttention", "ring_step", "ring_schedule", "split_sequence",
+    "ring_attention_all_ranks",
 ]

@@ -87,6 +87,12 @@ SIGNATURES = {
         _p, _i32,                                    # row_base, row0
         _p,                                          # stream
     ]),
+    "nq_attn_merge": (_i32, [
+        _p, _i64p, _p,                               # o, o_strides, lse
+        _p, _i64p, _p,                               # o_part, part_strides, lse_part
+        _i32, _i32, _i32, _i32, _i32,                # B, H, S, D, dtype
+        _p,                                          # stream
+    ]),
 }
 
 _lock = threading.Lock()

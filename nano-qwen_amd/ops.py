@@ -29,6 +29,7 @@ __all__ = [
     "attention_decode",
     "attention_decode_paged",
     "kv_append_paged",
+    "attention_merge_",
     "decode_workspace_bytes",
     "flash_attention",
     "apply_rope",
@@ -498,6 +499,33 @@ def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
                       "nq_attn_decode_paged_fwd",
                       (q, k_new, v_new, bt, lens_t, workspace, cos_t, sin_t, qp, qw, kw,
                        q_str, o_str, kn_str, vn_str), out)
+    return call if plan else call.launch()
+
+
+def attention_merge_(o: torch.Tensor, lse: torch.Tensor, o_part: torch.Tensor,
+                     lse_part: torch.Tensor, plan: bool = False):
+    """Merge a partial (o_part, lse_part) into (o, lse) in place.
+
+    Both are attention over disjoint key sets: o/o_part (B, H, S, D)
+    normalised outputs, lse/lse_part fp32 (B, H, S) natural-log sum-exp of the
+    scaled scores (``attention_prefill(..., return_lse=True)``).  The
+    online-softmax combine of ring attention (distributed/context_parallel.py:
+    120-127).  Returns (o, lse).
+    """
+    _require_device(o, lse, o_part, lse_part)
+    B, H, S, D = o.shape
+    if tuple(o_part.shape) != (B, H, S, D) or o_part.dtype != o.dtype:
+        raise ValueError("o_part must match o in shape and dtype")
+    for name, t in (("lse", lse), ("lse_part", lse_part)):
+        if tuple(t.shape) != (B, H, S) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 (B, H, S) tensor")
+    _rows_out(o, "o")
+    o_part = _rows_in(o_part)
+    st = _lib.strides3
+    args = (_ptr(o), st(o.stride()[:3]), _ptr(lse), _ptr(o_part), st(o_part.stride()[:3]),
+            _ptr(lse_part), B, H, S, D, _code(o), _stream(o))
+    call = KernelCall(_lib.load().nq_attn_merge, args, len(args) - 1, "nq_attn_merge",
+                      (o_part, lse_part), (o, lse))
     return call if plan else call.launch()
 
 

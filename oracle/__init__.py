@@ -25,3 +25,8 @@ from .model_oracle import (  # noqa: F401
     greedy_reference_protocol,
     greedy_full_recompute,
 )
+from .ring_oracle import (  # noqa: F401
+    ring_attention,
+    merge_partials,
+    attention_lse,
+)
