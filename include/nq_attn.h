@@ -221,6 +221,47 @@ int nq_attn_merge(void* o, const int64_t* o_strides, float* lse, const void* o_p
                   const int64_t* part_strides, const float* lse_part, int B, int H, int S, int D,
                   int dtype, void* stream);
 
+/* Bytes of fp32 workspace nq_attn_bwd needs (the per-row Delta = rowsum(dO * O)). */
+int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S);
+
+/*
+ * Attention backward (FlashAttention-2 with the forward's LSE): the gradient
+ * of F.scaled_dot_product_attention (model/attention.py:110-115) that
+ * training's loss.backward() runs today, for GQA without the
+ * repeat_interleave (the kv-head gradients are summed over their G query
+ * heads).
+ *
+ * q, k, v: the forward's operands as the attention saw them (Q-hat and K-hat,
+ *   i.e. after QK-Norm and RoPE), (B, H, S|T, D) with strides {batch, head,
+ *   seq}; o, dout: (B, Hq, S, D) forward output and its gradient; lse: fp32
+ *   (B, Hq, S) from nq_attn_prefill_fwd (same q, k, v, causal and sm_scale).
+ * dq (B, Hq, S, D), dk / dv (B, Hkv, T, D): outputs, fully written.
+ * causal keeps key j for query i iff j <= i + T - S (needs S <= T).
+ * workspace: nq_attn_bwd_workspace_bytes(B, Hq, S) bytes.
+ * Requires 128 % (Hq / Hkv) == 0.  Storage dtype bf16 or fp32 (products on
+ * bf16 MFMA, accumulation and softmax in fp32).
+ */
+int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
+                const void* dout, const int64_t* do_strides, const float* lse, void* dq,
+                const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
+                int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream);
+
+/*
+ * Backward of QK-Norm + RoPE (model/norm.py:17-22 and model/rope.py:133-161
+ * as applied at attention.py:95-100): given the pre-norm rows x and the
+ * gradient dy of y = rope(rmsnorm(x) * weight), writes dx and ADDS the weight
+ * gradient into dweight (fp32, D elements; the caller zeroes it).  weight /
+ * dweight NULL: no norm; cos_tab NULL: no rotation.  Positions as in
+ * nq_qk_norm_rope.  x, dy, dx: (B, H, S, D) with strides {batch, head, seq}.
+ */
+int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, const void* dy,
+                        const int64_t* dy_strides, void* dx, const int64_t* dx_strides,
+                        const float* weight, float* dweight, int B, int S, int H, int D, int dtype,
+                        float eps, const float* cos_tab, const float* sin_tab, int max_pos,
+                        const int32_t* pos, const int32_t* pos_base, int pos0, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

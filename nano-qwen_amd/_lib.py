@@ -93,6 +93,23 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32,                # B, H, S, D, dtype
         _p,                                          # stream
     ]),
+    "nq_attn_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "nq_attn_bwd": (_i32, [
+        _p, _i64p, _p, _i64p, _p, _i64p,             # q, k, v (+ strides)
+        _p, _i64p, _p, _i64p, _p,                    # o, dout (+ strides), lse
+        _p, _i64p, _p, _i64p, _p, _i64p,             # dq, dk, dv (+ strides)
+        _p, _i64,                                    # workspace, workspace_bytes
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype
+        _i32, _f32, _p,                              # causal, sm_scale, stream
+    ]),
+    "nq_qk_norm_rope_bwd": (_i32, [
+        _p, _i64p, _p, _i64p, _p, _i64p,             # x, dy, dx (+ strides)
+        _p, _p,                                      # weight, dweight
+        _i32, _i32, _i32, _i32, _i32,                # B, S, H, D, dtype
+        _f32, _p, _p, _i32,                          # eps, cos, sin, max_pos
+        _p, _p, _i32,                                # pos, pos_base, pos0
+        _p,                                          # stream
+    ]),
 }
 
 _lock = threading.Lock()

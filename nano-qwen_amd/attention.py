@@ -13,9 +13,12 @@ Dispatch (following kernels/flash_attn.py:139's convention):
     one row-kernel launch (K-Norm + RoPE -> K-hat, plus the V copy when a
     cache is used), then the prefill kernel (Q-Norm + RoPE fused into the Q
     load), or the split-K decode kernel when a cache is present and S == 1;
-  * autograd or an explicit attention_mask -> torch ops on the device, the
-    reference's own arithmetic (SDPA), since the kernels are forward-only and
-    maskless;
+  * autograd (training, no cache) -> the same kernels through an autograd
+    Function whose backward is the FlashAttention-2 backward kernels plus the
+    QK-Norm + RoPE backward kernel (nano_qwen_amd.autograd);
+  * an explicit attention_mask, attention dropout, or autograd with a cache
+    -> torch ops on the device, the reference's own arithmetic (SDPA), since
+    the kernels are maskless;
   * host tensors -> RuntimeError (the kernels are the product; there is no
     CPU path).
 
@@ -37,13 +40,13 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops
+from . import autograd, ops
 from .config import num_kv_groups
 from .norm import RMSNorm
 from .rope import RotaryEmbedding
 
 # Counters of which path forward() took (kernel launches vs torch fallback).
-stats = {"kernel_forward": 0, "torch_forward": 0}
+stats = {"kernel_forward": 0, "kernel_train_forward": 0, "torch_forward": 0}
 
 
 class KVCache:
@@ -333,19 +336,27 @@ class Attention(nn.Module):
         k = self.k_proj(hidden_states)
         v = self.v_proj(hidden_states)
         dropout = self.training and getattr(self.config, "attention_dropout", 0.0) > 0
-        needs_grad = q.requires_grad or k.requires_grad or v.requires_grad
-        if attention_mask is not None or needs_grad or dropout:
+        qw = self.q_norm.weight if self.qk_norm else None
+        kw = self.k_norm.weight if self.qk_norm else None
+        needs_grad = torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (q, k, v, qw, kw))
+        if attention_mask is not None or dropout or (needs_grad and kv_cache is not None):
             stats["torch_forward"] += 1
             return self._torch_forward(q, k, v, position_ids, attention_mask, kv_cache)
-        stats["kernel_forward"] += 1
 
         q4 = q.view(B, S, H, D).transpose(1, 2)
         k4 = k.view(B, S, Hkv, D).transpose(1, 2)
         v4 = v.view(B, S, Hkv, D).transpose(1, 2)
         cos, sin = self.rotary_emb.tables_f32()
-        qw = self.q_norm.weight if self.qk_norm else None
-        kw = self.k_norm.weight if self.qk_norm else None
         eps = self.config.rms_norm_eps
+        if needs_grad:
+            # training: the forward and backward both on the kernels (causal,
+            # no cache: attention.py:113 with kv_cache None)
+            stats["kernel_train_forward"] += 1
+            o = autograd.attention_core(q4, k4, v4, qw, kw, cos=cos, sin=sin,
+                                        position_ids=position_ids, eps=eps, causal=True)
+            return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
+        stats["kernel_forward"] += 1
         if isinstance(kv_cache, PagedKVCache):
             return self._paged_forward(q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps)
         past = kv_cache.seq_len if kv_cache is not None else 0

@@ -530,6 +530,90 @@ def attention_merge_(o: torch.Tensor, lse: torch.Tensor, o_part: torch.Tensor,
 
 
 # ---------------------------------------------------------------------------
+# Backward
+# ---------------------------------------------------------------------------
+
+def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                       dout: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
+                       sm_scale: Optional[float] = None,
+                       workspace: Optional[torch.Tensor] = None, plan: bool = False):
+    """FlashAttention-2 backward: (dq, dk, dv) of o = softmax(scale q k^T) v.
+
+    q: (B, Hq, S, D), k/v: (B, Hkv, T, D) as the forward attended them (after
+    QK-Norm and RoPE); o, dout: (B, Hq, S, D); lse: the forward's fp32
+    (B, Hq, S) log-sum-exp (``attention_prefill(..., return_lse=True)`` with
+    the same causal and sm_scale).  dk/dv sum the gradients of the G query
+    heads that share a kv head.  Returns fresh (dq, dk, dv) in q's dtype.
+    """
+    _require_device(q, k, v, o, dout, lse)
+    B, Hq, S, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("k/v do not match q")
+    if tuple(o.shape) != (B, Hq, S, D) or tuple(dout.shape) != (B, Hq, S, D):
+        raise ValueError("o and dout must be (B, Hq, S, D)")
+    for t in (k, v, o, dout):
+        if t.dtype != q.dtype:
+            raise TypeError("q, k, v, o and dout must share one dtype")
+    if tuple(lse.shape) != (B, Hq, S) or lse.dtype != torch.float32:
+        raise ValueError("lse must be fp32 (B, Hq, S)")
+    q, k, v, o, dout = (_rows_in(t) for t in (q, k, v, o, dout))
+    lse = lse.contiguous()
+    dev = q.device
+    dq = torch.empty(B, S, Hq, D, dtype=q.dtype, device=dev).transpose(1, 2)
+    dk = torch.empty(B, T, Hkv, D, dtype=q.dtype, device=dev).transpose(1, 2)
+    dv = torch.empty(B, T, Hkv, D, dtype=q.dtype, device=dev).transpose(1, 2)
+    lib = _lib.load()
+    need = int(lib.nq_attn_bwd_workspace_bytes(B, Hq, S))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    st = _lib.strides3
+    args = (
+        _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
+        _ptr(o), st(o.stride()[:3]), _ptr(dout), st(dout.stride()[:3]), _ptr(lse),
+        _ptr(dq), st(dq.stride()[:3]), _ptr(dk), st(dk.stride()[:3]), _ptr(dv), st(dv.stride()[:3]),
+        _ptr(workspace), workspace.numel() * workspace.element_size(),
+        B, Hq, Hkv, S, T, D, _code(q), int(bool(causal)),
+        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    call = KernelCall(lib.nq_attn_bwd, args, len(args) - 1, "nq_attn_bwd",
+                      (q, k, v, o, dout, lse, workspace), (dq, dk, dv))
+    return call if plan else call.launch()
+
+
+def qk_norm_rope_backward(x: torch.Tensor, dy: torch.Tensor, *, weight: Optional[torch.Tensor] = None,
+                          eps: float = 1e-6, cos: Optional[torch.Tensor] = None,
+                          sin: Optional[torch.Tensor] = None,
+                          position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
+                          pos_base: Optional[torch.Tensor] = None):
+    """Backward of y = rope(rmsnorm(x) * weight) over (B, H, S, D) rows.
+
+    Returns (dx, dweight): dx in x's dtype, dweight fp32 (D,) summed over all
+    rows (None without a weight).  Positions as in ``qk_norm_rope``.
+    """
+    _require_device(x, dy)
+    B, H, S, D = x.shape
+    if tuple(dy.shape) != (B, H, S, D) or dy.dtype != x.dtype:
+        raise ValueError("dy must match x")
+    x, dy = _rows_in(x), _rows_in(dy)
+    dev = x.device
+    dx = torch.empty(B, S, H, D, dtype=x.dtype, device=dev).transpose(1, 2)
+    w = _f32(weight, dev)
+    dw = torch.zeros(D, dtype=torch.float32, device=dev) if w is not None else None
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    pos = _i32(position_ids, dev)
+    if pos is not None and tuple(pos.shape) != (B, S):
+        pos = pos.expand(B, S).contiguous()
+    pb = _i32(pos_base, dev)
+    st = _lib.strides3
+    rc = _lib.load().nq_qk_norm_rope_bwd(
+        _ptr(x), st(x.stride()[:3]), _ptr(dy), st(dy.stride()[:3]), _ptr(dx), st(dx.stride()[:3]),
+        _ptr(w), _ptr(dw), B, S, H, D, _code(x), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
+        _ptr(pos), _ptr(pb), int(pos_offset), _stream(x))
+    _lib.check(rc, "nq_qk_norm_rope_bwd")
+    return dx, dw
+
+
+# ---------------------------------------------------------------------------
 # Mirrors of the reference kernel API
 # ---------------------------------------------------------------------------
 
@@ -538,17 +622,15 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
     """kernels/flash_attn.py:130-143 on the gfx950 prefill kernel.
 
     q: (B, H, N, D), k/v: (B, Hkv, N, D) with H % Hkv == 0 (the reference
-    requires Hkv == H; GQA is accepted here).  Like the reference, inputs that
-    require grad take torch's SDPA instead (flash_attn.py:139).  Returns a
-    contiguous (B, H, N, D) tensor.
+    requires Hkv == H; GQA is accepted here).  Where the reference hands inputs
+    that require grad to torch's SDPA (flash_attn.py:139), this runs them
+    through the kernels' autograd Function (FlashAttention-2 backward).
+    Returns a contiguous (B, H, N, D) tensor.
     """
     _require_device(q, k, v)
-    if q.requires_grad or k.requires_grad or v.requires_grad:
-        G = q.shape[1] // k.shape[1]
-        kk = k.repeat_interleave(G, 1) if G > 1 else k
-        vv = v.repeat_interleave(G, 1) if G > 1 else v
-        return torch.nn.functional.scaled_dot_product_attention(q, kk, vv, is_causal=causal,
-                                                                scale=sm_scale)
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        from .autograd import flash_attention_train
+        return flash_attention_train(q, k, v, causal=causal, sm_scale=sm_scale)
     B, H, N, D = q.shape
     out = torch.empty_like(q, memory_format=torch.contiguous_format)
     return attention_prefill(q, k, v, causal=causal, sm_scale=sm_scale, out=out)

@@ -1,0 +1,187 @@
+"""GPU parity of the attention backward and the QK-Norm + RoPE backward.
+
+References are torch autograd in fp64 on the CPU through the oracle's
+functions (``attention``, ``rms_norm``, ``rotate_half``, pinned by the
+oracle tests), on the same bf16-valued (or fp32) inputs.
+
+Tolerance for gradients, relative to the largest reference magnitude of the
+same tensor: max-abs <= 2e-2 * max|ref| and mean-abs <= 2e-3 * max|ref| (the
+bf16 gate of the forward, scaled to the tensor), for bf16 and fp32 storage
+alike, since the products run on bf16 MFMA either way.
+"""
+
+import pytest
+import torch
+
+import nano_qwen_amd as nq
+from nano_qwen_amd import ops
+from oracle import attention, attention_module_forward, rms_norm, rope_tables, rotate_half
+from tests.helpers import randn, say
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _close_rel(got, ref, what, dtype=torch.bfloat16):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    scale = float(ref.abs().max())
+    mx_tol, mean_tol = 2e-2, 2e-3
+    d = (got - ref).abs()
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    assert float(d.max()) <= mx_tol * scale and float(d.mean()) <= mean_tol * scale, \
+        f"{what}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {scale:.3e})"
+
+
+def _ref_grads(q, k, v, do, causal, scale=None):
+    qd, kd, vd = (t.detach().double().cpu().requires_grad_(True) for t in (q, k, v))
+    S, T = q.shape[2], k.shape[2]
+    o = attention(qd, kd, vd, causal=causal, causal_offset=T - S, scale=scale,
+                  compute_dtype=torch.float64)
+    o.backward(do.double().cpu())
+    return o.detach(), qd.grad, kd.grad, vd.grad
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 2), (16, 1)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_backward_against_fp64_autograd(D, Hq, Hkv, causal):
+    say(f"bwd D={D} {Hq}/{Hkv} causal={causal}")
+    B, S = 2, 200
+    q = randn(B, Hq, S, D, seed=501, dtype=torch.bfloat16)
+    k = randn(B, Hkv, S, D, seed=502, dtype=torch.bfloat16)
+    v = randn(B, Hkv, S, D, seed=503, dtype=torch.bfloat16)
+    do = randn(B, Hq, S, D, seed=504, dtype=torch.bfloat16)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=causal)
+    _, rq, rk, rv = _ref_grads(q, k, v, do, causal)
+    _close_rel(dq, rq, "dq")
+    _close_rel(dk, rk, "dk")
+    _close_rel(dv, rv, "dv")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attention_backward_bottom_right_causal_and_dtypes(dtype):
+    """S < T (queries are the last S positions), ragged sizes, fp32 storage too."""
+    say(f"bwd S<T {dtype}")
+    B, Hq, Hkv, S, T, D = 1, 8, 4, 77, 301, 128
+    q = randn(B, Hq, S, D, seed=511, dtype=dtype)
+    k = randn(B, Hkv, T, D, seed=512, dtype=dtype)
+    v = randn(B, Hkv, T, D, seed=513, dtype=dtype)
+    do = randn(B, Hq, S, D, seed=514, dtype=dtype)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=True)
+    # the kernels round fp32 K/V (and the MFMA operands) to bf16: the reference sees the same rounding
+    kr, vr = (k.bfloat16().to(dtype), v.bfloat16().to(dtype)) if dtype == torch.float32 else (k, v)
+    _, rq, rk, rv = _ref_grads(q, kr, vr, do, True)
+    for got, ref, name in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+        _close_rel(got, ref, name, dtype)
+
+
+def test_attention_backward_long_sequence():
+    """B1 S2048 16/8 D128 causal, every gradient element against fp64 autograd."""
+    say("bwd S=2048")
+    B, Hq, Hkv, S, D = 1, 16, 8, 2048, 128
+    q = randn(B, Hq, S, D, seed=521, dtype=torch.bfloat16)
+    k = randn(B, Hkv, S, D, seed=522, dtype=torch.bfloat16)
+    v = randn(B, Hkv, S, D, seed=523, dtype=torch.bfloat16)
+    do = randn(B, Hq, S, D, seed=524, dtype=torch.bfloat16)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=True)
+    _, rq, rk, rv = _ref_grads(q, k, v, do, True)
+    _close_rel(dq, rq, "dq S=2048")
+    _close_rel(dk, rk, "dk S=2048")
+    _close_rel(dv, rv, "dv S=2048")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+def test_norm_rope_backward_against_fp64_autograd(dtype, D):
+    say(f"norm+rope bwd D={D} {dtype}")
+    B, H, S = 2, 3, 50
+    x = randn(B, H, S, D, seed=531, dtype=dtype, scale=2.0)
+    dy = randn(B, H, S, D, seed=532, dtype=dtype)
+    w = 1 + 0.1 * randn(D, seed=533)
+    cos, sin = rope_tables(D, 512, 1e6)
+    pos = torch.randint(0, 512, (B, S), generator=torch.Generator().manual_seed(534))
+    dx, dw = ops.qk_norm_rope_backward(x.to(DEV), dy.to(DEV), weight=w.to(DEV), eps=1e-6,
+                                       cos=cos.to(DEV), sin=sin.to(DEV), position_ids=pos.to(DEV))
+    xd = x.double().requires_grad_(True)
+    wd = w.double().requires_grad_(True)
+    y = rotate_half(rms_norm(xd, wd, 1e-6, compute_dtype=torch.float64),
+                    cos.double()[pos][:, None], sin.double()[pos][:, None])
+    y.backward(dy.double())
+    _close_rel(dx, xd.grad, "dx", dtype)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
+    torch.testing.assert_close(dw.double().cpu(), wd.grad, rtol=tol, atol=tol * float(wd.grad.abs().max()))
+
+
+def test_flash_attention_mirror_autograd():
+    say("flash_attention autograd")
+    B, H, S, D = 2, 4, 96, 64
+    q = randn(B, H, S, D, seed=541, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    k = randn(B, H, S, D, seed=542, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    v = randn(B, H, S, D, seed=543, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    do = randn(B, H, S, D, seed=544, dtype=torch.bfloat16)
+    o = nq.flash_attention(q, k, v, causal=True)
+    assert o.is_contiguous()
+    o.backward(do.to(DEV))
+    _, rq, rk, rv = _ref_grads(q, k, v, do, True)
+    _close_rel(q.grad, rq, "flash dq")
+    _close_rel(k.grad, rk, "flash dk")
+    _close_rel(v.grad, rv, "flash dv")
+
+
+def _module_grads(weights, h, g, pos, cos, sin, dtype, H, Hkv, D):
+    """Oracle module forward + backward on the CPU in ``dtype`` (the reference's dtype flow)."""
+    w = {n: t.detach().to(dtype).clone().requires_grad_(True) for n, t in weights.items()}
+    out, _ = attention_module_forward(h.to(dtype), w, num_heads=H, num_kv_heads=Hkv, head_dim=D, eps=1e-6,
+                                      cos_table=cos.to(dtype), sin_table=sin.to(dtype), position_ids=pos)
+    out.backward(g.to(dtype))
+    return out.detach().double(), {n: t.grad.double() for n, t in w.items()}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_module_training_gradients_against_oracle(dtype):
+    """Attention.forward + backward on the kernels against the oracle module under autograd.
+
+    fp32 module: within the relative bound above of fp64 autograd.  bf16
+    module: no further from fp64 autograd than the reference's own arithmetic
+    run in bf16 (the oracle module in bf16 on the CPU, the dtype flow of
+    model/attention.py under SDPA autograd) is, within a factor 1.5.
+    """
+    say(f"module train grads {dtype}")
+    hidden, H, Hkv, D, B, S = 256, 8, 2, 64, 2, 80
+    cfg = nq.AttentionConfig(hidden_size=hidden, num_attention_heads=H, num_key_value_heads=Hkv,
+                             head_dim=D, max_position_embeddings=256)
+    torch.manual_seed(0)
+    attn = nq.Attention(cfg)
+    with torch.no_grad():
+        attn.q_norm.weight.add_(0.1 * torch.randn(D))
+        attn.k_norm.weight.add_(0.1 * torch.randn(D))
+    attn = attn.to(DEV, dtype).train()
+    # the references take the module's own (possibly bf16-rounded) weights
+    names = ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")
+    weights = {n: getattr(attn, n).weight.detach().cpu() for n in names}
+    h = randn(B, S, hidden, seed=551, dtype=dtype)
+    g = randn(B, S, hidden, seed=552, dtype=dtype)
+    pos = torch.stack([torch.arange(S) + 3, torch.arange(S) * 2])
+    out = attn(h.to(DEV), position_ids=pos.to(DEV))
+    out.backward(g.to(DEV))
+    cos, sin = rope_tables(D, 256, 1e6)
+    ref_out, ref_g = _module_grads(weights, h, g, pos, cos, sin, torch.float64, H, Hkv, D)
+    if dtype == torch.float32:
+        _close_rel(out, ref_out, "module out", dtype)
+        for n in names:
+            _close_rel(getattr(attn, n).weight.grad, ref_g[n], f"grad {n}", dtype)
+        return
+    _, bf_g = _module_grads(weights, h, g, pos, cos, sin, torch.bfloat16, H, Hkv, D)
+    for n in names:
+        got = getattr(attn, n).weight.grad.double().cpu()
+        e_k = (got - ref_g[n]).abs()
+        e_r = (bf_g[n] - ref_g[n]).abs()
+        floor = 1e-3 * float(ref_g[n].abs().max())
+        assert float(e_k.mean()) <= 1.5 * float(e_r.mean()) + floor, \
+            f"grad {n}: mean error {float(e_k.mean()):.3e}, reference bf16 autograd {float(e_r.mean()):.3e}"
+        assert float(e_k.max()) <= 1.5 * float(e_r.max()) + floor, \
+            f"grad {n}: max error {float(e_k.max()):.3e}, reference bf16 autograd {float(e_r.max()):.3e}"

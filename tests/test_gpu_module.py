@@ -112,12 +112,17 @@ def test_mask_takes_torch_path_and_matches(fx):
     np.testing.assert_allclose(out.cpu().numpy(), fx["mask_out"], rtol=1e-4, atol=1e-4)
 
 
-def test_autograd_takes_torch_path():
-    say("module autograd (torch path)")
+def test_autograd_runs_on_the_kernels():
+    say("module autograd (kernel path)")
     attn, h = _module()
+    before = dict(nq.stats)
     out = attn(h)
     out.float().pow(2).mean().backward()
-    assert attn.q_proj.weight.grad is not None and torch.isfinite(attn.q_proj.weight.grad).all()
+    assert nq.stats["kernel_train_forward"] == before["kernel_train_forward"] + 1
+    assert nq.stats["torch_forward"] == before["torch_forward"]
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm"):
+        g = getattr(attn, name).weight.grad
+        assert g is not None and torch.isfinite(g).all(), name
 
 
 @torch.no_grad()
