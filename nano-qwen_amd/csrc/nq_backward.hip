@@ -26,8 +26,9 @@
 // with no data movement, and its A operand (K^T, dO^T or Q^T) is read from the
 // row-major LDS tile with ds_read_b64_tr_b16.
 //
-// This version stages every tile through LDS with one buffer and a barrier on
-// each side (the second resident workgroup of the CU overlaps the loads).
+// Tiles are double-buffered in LDS: bf16 tiles travel HBM -> LDS with
+// global_load_lds (one tile ahead), one barrier per tile; the transpose reads
+// are issued as inline asm so that the loads in flight are not waited for.
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
@@ -71,21 +72,6 @@ struct BwTile {
   __device__ static int tsw(int r, int c) { return c ^ (4 * ((r / RPL) & (D / 32 - 1))); }
 };
 
-// Stage rows [r0, r0 + NR) of a strided (row stride `rs` elements) source into
-// a row-major LDS tile with chunk swizzle SW; rows >= nvalid are zero.
-template <int D, typename T, int NR, bool TRANSPOSE_SW>
-__device__ __forceinline__ void bw_stage(unsigned char* tile, const T* src, int64_t rs, int r0, int nvalid) {
-  using L = BwTile<D>;
-  constexpr int CH = NR * L::CPR;  // 16-byte chunks in the tile
-  for (int c = threadIdx.x; c < CH; c += 256) {
-    const int r = c / L::CPR, ch = c % L::CPR;
-    const int row = r0 + r;
-    bf16x8 val = row < nvalid ? to_bf16x8(Vec8<T>::load_f32(src + (int64_t)row * rs + ch * 8)) : bf16x8{};
-    const int pc = TRANSPOSE_SW ? L::tsw(r, ch) : L::rsw(r, ch);
-    *reinterpret_cast<bf16x8*>(tile + r * L::RB + pc * 16) = val;
-  }
-}
-
 // ---------------------------------------------------------------- Delta
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
@@ -109,17 +95,54 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
   }
 }
 
+// Stage a tile of NR rows (rows >= nvalid clamp to the last valid row; their
+// scores are masked) into LDS, swizzled.  bf16 storage: global_load_lds
+// (HBM -> LDS, no registers): instruction m of the tile fills LDS bytes
+// [m*1024, m*1024+1024), lane t the 16 bytes at +16t, so the lane loads the
+// logical chunk that belongs in that physical slot (the swizzle is an XOR,
+// its own inverse).  fp32 storage: loads converted in registers.
+template <int D, typename T, int NR, bool TSW>
+__device__ __forceinline__ void bw_tile(unsigned char* tile, const T* src, int64_t rs, int nvalid, int wave,
+                                        int lane) {
+  using L = BwTile<D>;
+  if constexpr (sizeof(T) == 2) {
+    constexpr int NI = NR * L::RB / 1024;
+    static_assert(NI % 4 == 0 || NI < 4, "tile size");
+    for (int m = wave; m < NI; m += 4) {
+      const int pbyte = m * 1024 + lane * 16;
+      const int r = pbyte / L::RB, pc = (pbyte % L::RB) / 16;
+      const int lc = TSW ? L::tsw(r, pc) : L::rsw(r, pc);
+      const int row = r < nvalid ? r : nvalid - 1;
+      global_load_lds16(src + (int64_t)row * rs + lc * 8, tile + m * 1024);
+    }
+  } else {
+    constexpr int CH = NR * L::CPR;
+    for (int c = threadIdx.x; c < CH; c += 256) {
+      const int r = c / L::CPR, ch = c % L::CPR;
+      const int row = r < nvalid ? r : nvalid - 1;
+      const bf16x8 val = to_bf16x8(Vec8<T>::load_f32(src + (int64_t)row * rs + ch * 8));
+      const int pc = TSW ? L::tsw(r, ch) : L::rsw(r, ch);
+      *reinterpret_cast<bf16x8*>(tile + r * L::RB + pc * 16) = val;
+    }
+  }
+}
+
+// Transpose-read operand: rows r0..r0+3 at `addr`, r0+4..r0+7 four rows on.
+template <int D>
+__device__ __forceinline__ bf16x8 bw_tr8(const unsigned char* p) {
+  return lds_read_tr8_nowait<8 * D>(lds_addr(p));
+}
+
 // ---------------------------------------------------------------- dQ
 template <int D, typename T, bool CAUSAL>
 __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
   using L = BwTile<D>;
   constexpr int NDB = D / 16, NDO = D / 32;
   constexpr int TB = BW_BN * L::RB;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TB];  // K (transpose swizzle), V
-  unsigned char* Kt = smem;
-  unsigned char* Vt = smem + TB;
+  // two buffers of (K tile with the transpose swizzle, V tile)
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TB];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r32 = lane & 31, hh = lane >> 5;
   const int npairs = p.B * p.Hkv;
   const int qrank = blockIdx.x / npairs, pair = blockIdx.x % npairs;
@@ -128,6 +151,15 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
   const int q0 = qblk * p.BM;
   const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + p.coff) : p.T;
   const int ntiles = (kv_end + BW_BN - 1) / BW_BN;
+
+  const T* kb0 = reinterpret_cast<const T*>(p.k) + b * p.ksb + kvh * p.ksh;
+  const T* vb0 = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
+  auto stage = [&](int j, int buf) {
+    const int n0 = j * BW_BN;
+    bw_tile<D, T, BW_BN, true>(smem + buf * 2 * TB, kb0 + (int64_t)n0 * p.kss, p.kss, p.T - n0, wave, lane);
+    bw_tile<D, T, BW_BN, false>(smem + buf * 2 * TB + TB, vb0 + (int64_t)n0 * p.vss, p.vss, p.T - n0, wave, lane);
+  };
+  stage(0, 0);  // its latency overlaps the Q / dO loads below
 
   const int R = wave * 32 + r32;
   const int g = R / p.BM, pr = R - g * p.BM;
@@ -147,7 +179,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
     }
   }
   const int64_t srow = ((int64_t)b * p.Hq + head) * p.S + qi_c;
-  const float lse2 = qvalid ? p.lse[srow] * kLog2e : INFINITY;  // invalid rows: P = 0
+  const float lse2 = p.lse[srow] * kLog2e;
   const float dlt = p.delta[srow];
 
   // LDS offsets: K / V rows through the key permutation (A of S^T and dP^T);
@@ -173,17 +205,18 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
   floatx16 dqacc[NDO];
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) dqacc[dd] = floatx16{};
-
-  const T* kb0 = reinterpret_cast<const T*>(p.k) + b * p.ksb + kvh * p.ksh;
-  const T* vb0 = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
-  const int lim = CAUSAL ? qi + p.coff : p.T - 1;  // last key this row sees
+  // last key this row sees (rows past S see none)
+  const int lim = !qvalid ? -1 : (CAUSAL ? min(qi + p.coff, p.T - 1) : p.T - 1);
 
   for (int j = 0; j < ntiles; ++j) {
     const int n0 = j * BW_BN;
+    // tile j has landed (each wave waits for its own loads, the barrier for
+    // everyone's); every wave is done with tile j-1, whose buffer is refilled
+    if constexpr (sizeof(T) == 2) wait_vmcnt0();
     __syncthreads();
-    bw_stage<D, T, BW_BN, true>(Kt, kb0 + (int64_t)n0 * p.kss, p.kss, 0, p.T - n0);
-    bw_stage<D, T, BW_BN, false>(Vt, vb0 + (int64_t)n0 * p.vss, p.vss, 0, p.T - n0);
-    __syncthreads();
+    if (j + 1 < ntiles) stage(j + 1, (j + 1) & 1);
+    const unsigned char* Kt = smem + (j & 1) * 2 * TB;
+    const unsigned char* Vt = Kt + TB;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       floatx16 s = floatx16{}, dp = floatx16{};
@@ -198,23 +231,24 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = n0 + kb * 32 + bw_cidx(i, hh);
-        const float pe = key <= lim && key < p.T ? fast_exp2(s[i] * p.scale_log2 - lse2) : 0.f;
+        // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
+        const float pe = fast_exp2(key <= lim ? __builtin_fmaf(s[i], p.scale_log2, -lse2) : -INFINITY);
         ds[i / 8][i % 8] = pe * (dp[i] - dlt);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const bf16x8 bds = to_bf16x8(ds[ks]);
+        bf16x8 ak[NDO];
 #pragma unroll
-        for (int dd = 0; dd < NDO; ++dd) {
-          const bf16* a = reinterpret_cast<const bf16*>(Kt + kto[dd] + (kb * 32 + ks * 16) * L::RB);
-          const bf16x8 ak = lds_read_tr8(a, a + 4 * D);  // rows +0..3 and +4..7 (4 rows = 4 * D elements)
-          dqacc[dd] = mfma32(ak, bds, dqacc[dd]);
-        }
+        for (int dd = 0; dd < NDO; ++dd) ak[dd] = bw_tr8<D>(Kt + kto[dd] + (kb * 32 + ks * 16) * L::RB);
+        lgkm_wait<0>();
+#pragma unroll
+        for (int dd = 0; dd < NDO; ++dd) dqacc[dd] = mfma32(ak[dd], bds, dqacc[dd]);
       }
     }
   }
 
-  if (!qvalid || g >= p.G) return;
+  if (!qvalid) return;
   T* out = reinterpret_cast<T*>(p.dq) + b * p.dqsb + head * p.dqsh + (int64_t)qi * p.dqss;
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd)
@@ -232,13 +266,12 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
   using L = BwTile<D>;
   constexpr int NDB = D / 16, NDO = D / 32;
   constexpr int TB = BW_BQ * L::RB;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TB + 2 * BW_BQ * 4];
-  unsigned char* Qt = smem;        // transpose swizzle (row reads and transpose reads)
-  unsigned char* Dt = smem + TB;   // dO, likewise
-  float* lse_t = reinterpret_cast<float*>(smem + 2 * TB);
-  float* dlt_t = lse_t + BW_BQ;
+  constexpr int BUF = 2 * TB + 2 * BW_BQ * 4;  // Q tile, dO tile, LSE*log2e, Delta
+  constexpr int VB = BW_KEYS * L::RB;          // the block's V rows (B operand of dP)
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * BUF + VB];
+  unsigned char* Vs = smem + 2 * BUF;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r32 = lane & 31, hh = lane >> 5;
   const int nkb = (p.T + BW_KEYS - 1) / BW_KEYS;
   const int kblk = blockIdx.x % nkb, pair = blockIdx.x / nkb;
@@ -247,17 +280,48 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
   const int key = k0 + wave * 32 + r32;  // this lane's key (C column)
   const int key_c = key < p.T ? key : p.T - 1;
 
-  // K and V of the lane's key as B operands (column = key, k = head dims)
-  bf16x8 kop[NDB], vop[NDB];
+  // the work list: (head g, query tile qt) for queries that see a key of this
+  // block (q + coff >= k0)
+  const int qstart = CAUSAL ? max(0, k0 - p.coff) / BW_BQ * BW_BQ : 0;
+  const int nqt = qstart < p.S ? (p.S - qstart + BW_BQ - 1) / BW_BQ : 0;
+  const int niter = p.G * nqt;
+  auto stage = [&](int it, int buf) {
+    const int g = it / nqt, qt = qstart + (it % nqt) * BW_BQ;
+    const int head = kvh * p.G + g;
+    unsigned char* base = smem + buf * BUF;
+    bw_tile<D, T, BW_BQ, true>(base, reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qt * p.qss,
+                               p.qss, p.S - qt, wave, lane);
+    bw_tile<D, T, BW_BQ, true>(base + TB,
+                               reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qt * p.doss,
+                               p.doss, p.S - qt, wave, lane);
+    if (threadIdx.x < 2 * BW_BQ) {  // LSE (log2 units) and Delta of the tile's rows (rows past S: masked)
+      const int r = threadIdx.x % BW_BQ;
+      const int q = min(qt + r, p.S - 1);
+      const int64_t srow = ((int64_t)b * p.Hq + head) * p.S + q;
+      float* dst = reinterpret_cast<float*>(base + 2 * TB);
+      if (threadIdx.x < BW_BQ) dst[r] = p.lse[srow] * kLog2e;
+      else dst[BW_BQ + r] = p.delta[srow];
+    }
+  };
+  // V of the block's keys stays in LDS (read as the B operand of dP each
+  // step); K of the lane's key is held in registers (B operand of S).  Both
+  // stagings are waited for at the top of the first iteration (a workgroup
+  // without work issues none, so none is left in flight at exit).
+  if (niter > 0) {
+    bw_tile<D, T, BW_KEYS, false>(Vs, reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh + (int64_t)k0 * p.vss,
+                                  p.vss, p.T - k0, wave, lane);
+    stage(0, 0);
+  }
+
+  bf16x8 kop[NDB];
   {
     const T* krow = reinterpret_cast<const T*>(p.k) + b * p.ksb + kvh * p.ksh + (int64_t)key_c * p.kss;
-    const T* vrow = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh + (int64_t)key_c * p.vss;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      kop[db] = to_bf16x8(Vec8<T>::load_f32(krow + db * 16 + hh * 8));
-      vop[db] = to_bf16x8(Vec8<T>::load_f32(vrow + db * 16 + hh * 8));
-    }
+    for (int db = 0; db < NDB; ++db) kop[db] = to_bf16x8(Vec8<T>::load_f32(krow + db * 16 + hh * 8));
   }
+  // V row of the lane's key in the block tile, chunk (2 db + hh) swizzled
+  const int vrow_l = wave * 32 + r32;
+  const int vrow_o = vrow_l * L::RB;
   const int prow = bw_perm32(r32);
   int rro[NDB];
 #pragma unroll
@@ -277,52 +341,56 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) dkacc[dd] = dvacc[dd] = floatx16{};
 
-  // queries that see any key of this block: q + coff >= k0
-  const int qstart = CAUSAL ? max(0, k0 - p.coff) / BW_BQ * BW_BQ : 0;
-  for (int g = 0; g < p.G; ++g) {
-    const int head = kvh * p.G + g;
-    const T* qh = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh;
-    const T* dh = reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh;
-    const int64_t sbase = ((int64_t)b * p.Hq + head) * p.S;
-    for (int qt = qstart; qt < p.S; qt += BW_BQ) {
-      __syncthreads();
-      bw_stage<D, T, BW_BQ, true>(Qt, qh + (int64_t)qt * p.qss, p.qss, 0, p.S - qt);
-      bw_stage<D, T, BW_BQ, true>(Dt, dh + (int64_t)qt * p.doss, p.doss, 0, p.S - qt);
-      if (threadIdx.x < BW_BQ) {
-        const int q = qt + threadIdx.x;
-        lse_t[threadIdx.x] = q < p.S ? p.lse[sbase + q] * kLog2e : INFINITY;  // padding rows: P = 0
-        dlt_t[threadIdx.x] = q < p.S ? p.delta[sbase + q] : 0.f;
-      }
-      __syncthreads();
-      floatx16 s = floatx16{}, dp = floatx16{};
+  for (int it = 0; it < niter; ++it) {
+    const int qt = qstart + (it % nqt) * BW_BQ;
+    if constexpr (sizeof(T) == 2) wait_vmcnt0();
+    __syncthreads();
+    if (it + 1 < niter) stage(it + 1, (it + 1) & 1);
+    const unsigned char* Qt = smem + (it & 1) * BUF;
+    const unsigned char* Dt = Qt + TB;
+    const float* lse_t = reinterpret_cast<const float*>(Qt + 2 * TB);
+    const float* dlt_t = lse_t + BW_BQ;
+    floatx16 s = floatx16{}, dp = floatx16{};
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(Qt + rro[db]);
-        const bf16x8 ad = *reinterpret_cast<const bf16x8*>(Dt + rro[db]);
-        s = mfma32(aq, kop[db], s);
-        dp = mfma32(ad, vop[db], dp);
-      }
-      floatx8 pv[2], ds[2];
+    for (int db = 0; db < NDB; ++db) {
+      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(Qt + rro[db]);
+      const bf16x8 ad = *reinterpret_cast<const bf16x8*>(Dt + rro[db]);
+      const bf16x8 bv = *reinterpret_cast<const bf16x8*>(Vs + vrow_o + L::rsw(vrow_l, 2 * db + hh) * 16);
+      s = mfma32(aq, kop[db], s);
+      dp = mfma32(ad, bv, dp);
+    }
+    // this lane's 16 query rows: hh*8 + 0..7 and 16 + hh*8 + 0..7, four at a time
+    floatx8 pv[2], ds[2];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int qr = bw_cidx(i, hh);
-        const int q = qt + qr;
-        const bool keep = key < p.T && (!CAUSAL || key <= q + p.coff);
-        const float pe = keep ? fast_exp2(s[i] * p.scale_log2 - lse_t[qr]) : 0.f;
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int r0 = (i4 < 2 ? 0 : 16) + hh * 8 + (i4 & 1) * 4;
+      const floatx4 lv = *reinterpret_cast<const floatx4*>(lse_t + r0);
+      const floatx4 dv4 = *reinterpret_cast<const floatx4*>(dlt_t + r0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i4 * 4 + u;
+        const int q = qt + r0 + u;
+        const bool keep = key < p.T && q < p.S && (!CAUSAL || key <= q + p.coff);
+        const float pe = fast_exp2(keep ? __builtin_fmaf(s[i], p.scale_log2, -lv[u]) : -INFINITY);
         pv[i / 8][i % 8] = pe;
-        ds[i / 8][i % 8] = pe * (dp[i] - dlt_t[qr]);
+        ds[i / 8][i % 8] = pe * (dp[i] - dv4[u]);
       }
+    }
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 bp = to_bf16x8(pv[ks]);
-        const bf16x8 bds = to_bf16x8(ds[ks]);
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8 bp = to_bf16x8(pv[ks]);
+      const bf16x8 bds = to_bf16x8(ds[ks]);
+      bf16x8 ad[NDO], aq[NDO];
 #pragma unroll
-        for (int dd = 0; dd < NDO; ++dd) {
-          const bf16* ad = reinterpret_cast<const bf16*>(Dt + tro[dd] + ks * 16 * L::RB);
-          const bf16* aq = reinterpret_cast<const bf16*>(Qt + tro[dd] + ks * 16 * L::RB);
-          dvacc[dd] = mfma32(lds_read_tr8(ad, ad + 4 * D), bp, dvacc[dd]);
-          dkacc[dd] = mfma32(lds_read_tr8(aq, aq + 4 * D), bds, dkacc[dd]);
-        }
+      for (int dd = 0; dd < NDO; ++dd) {
+        ad[dd] = bw_tr8<D>(Dt + tro[dd] + ks * 16 * L::RB);
+        aq[dd] = bw_tr8<D>(Qt + tro[dd] + ks * 16 * L::RB);
+      }
+      lgkm_wait<0>();
+#pragma unroll
+      for (int dd = 0; dd < NDO; ++dd) {
+        dvacc[dd] = mfma32(ad[dd], bp, dvacc[dd]);
+        dkacc[dd] = mfma32(aq[dd], bds, dkacc[dd]);
       }
     }
   }
