@@ -42,7 +42,10 @@ struct BwdParams {
   const void* o;
   const void* dout;
   const float* lse;  // (B, Hq, S) natural log
-  float* delta;      // (B, Hq, S) scratch, written by bwd_delta_kernel
+  // scratch written by bwd_delta_kernel: per (batch, head) and 32-row query
+  // tile, 64 floats = [32 x LSE * log2(e) | 32 x Delta], rows past S zero
+  float* ws;
+  int nst;           // 32-row tiles per (batch, head)
   void* dq;
   void* dk;
   void* dv;
@@ -73,25 +76,39 @@ struct BwTile {
 };
 
 // ---------------------------------------------------------------- Delta
+// Index of (batch b, head h, query s) in the scratch: its LSE; Delta is 32 on.
+__device__ __forceinline__ int64_t bw_ws_index(const BwdParams& p, int b, int h, int s) {
+  return (((int64_t)b * p.Hq + h) * p.nst + s / 32) * 64 + (s & 31);
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
   constexpr int LPR = D / 8;
   constexpr int RPB = 256 / LPR;
   const int sub = threadIdx.x % LPR;
-  const int64_t nrows = (int64_t)p.B * p.Hq * p.S;
+  const int SP = p.nst * 32;  // padded rows per (batch, head)
+  const int64_t nrows = (int64_t)p.B * p.Hq * SP;
   for (int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; row < nrows; row += (int64_t)gridDim.x * RPB) {
-    const int s = (int)(row % p.S);
-    const int h = (int)((row / p.S) % p.Hq);
-    const int b = (int)(row / ((int64_t)p.S * p.Hq));
-    const floatx8 o = Vec8<T>::load_f32(reinterpret_cast<const T*>(p.o) + b * p.osb + h * p.osh + s * p.oss + sub * 8);
-    const floatx8 d =
-        Vec8<T>::load_f32(reinterpret_cast<const T*>(p.dout) + b * p.dosb + h * p.dosh + s * p.doss + sub * 8);
-    float acc = 0.f;
+    const int s = (int)(row % SP);
+    const int h = (int)((row / SP) % p.Hq);
+    const int b = (int)(row / ((int64_t)SP * p.Hq));
+    float acc = 0.f, l2 = 0.f;
+    if (s < p.S) {
+      const floatx8 o =
+          Vec8<T>::load_f32(reinterpret_cast<const T*>(p.o) + b * p.osb + h * p.osh + s * p.oss + sub * 8);
+      const floatx8 d =
+          Vec8<T>::load_f32(reinterpret_cast<const T*>(p.dout) + b * p.dosb + h * p.dosh + s * p.doss + sub * 8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(o[e], d[e], acc);
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(o[e], d[e], acc);
 #pragma unroll
-    for (int m = 1; m < LPR; m <<= 1) acc += shfl_xor_f(acc, m);
-    if (sub == 0) p.delta[row] = acc;
+      for (int m = 1; m < LPR; m <<= 1) acc += shfl_xor_f(acc, m);
+      l2 = p.lse[((int64_t)b * p.Hq + h) * p.S + s] * kLog2e;
+    }
+    if (sub == 0) {
+      const int64_t w = bw_ws_index(p, b, h, s);
+      p.ws[w] = l2;
+      p.ws[w + 32] = acc;
+    }
   }
 }
 
@@ -178,9 +195,9 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
       dop[db] = to_bf16x8(Vec8<T>::load_f32(drow + db * 16 + hh * 8));
     }
   }
-  const int64_t srow = ((int64_t)b * p.Hq + head) * p.S + qi_c;
-  const float lse2 = p.lse[srow] * kLog2e;
-  const float dlt = p.delta[srow];
+  const int64_t wi = bw_ws_index(p, b, head, qi_c);
+  const float lse2 = p.ws[wi];
+  const float dlt = p.ws[wi + 32];
 
   // LDS offsets: K / V rows through the key permutation (A of S^T and dP^T);
   // K^T through transpose reads (A of dQ^T)
@@ -294,14 +311,10 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
     bw_tile<D, T, BW_BQ, true>(base + TB,
                                reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qt * p.doss,
                                p.doss, p.S - qt, wave, lane);
-    if (threadIdx.x < 2 * BW_BQ) {  // LSE (log2 units) and Delta of the tile's rows (rows past S: masked)
-      const int r = threadIdx.x % BW_BQ;
-      const int q = min(qt + r, p.S - 1);
-      const int64_t srow = ((int64_t)b * p.Hq + head) * p.S + q;
-      float* dst = reinterpret_cast<float*>(base + 2 * TB);
-      if (threadIdx.x < BW_BQ) dst[r] = p.lse[srow] * kLog2e;
-      else dst[BW_BQ + r] = p.delta[srow];
-    }
+    // LSE (log2 units) and Delta of the tile's 32 rows: 256 contiguous bytes
+    // of the scratch, one 16-byte piece per lane of the last wave's first 16
+    if (wave == 3 && lane < 16)
+      global_load_lds16(p.ws + bw_ws_index(p, b, head, qt) + lane * 4, base + 2 * TB);
   };
   // V of the block's keys stays in LDS (read as the B operand of dP each
   // step); K of the lane's key is held in registers (B operand of S).  Both
@@ -343,7 +356,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 
   for (int it = 0; it < niter; ++it) {
     const int qt = qstart + (it % nqt) * BW_BQ;
-    if constexpr (sizeof(T) == 2) wait_vmcnt0();
+    wait_vmcnt0();  // the LSE / Delta rows always come through global_load_lds
     __syncthreads();
     if (it + 1 < niter) stage(it + 1, (it + 1) & 1);
     const unsigned char* Qt = smem + (it & 1) * BUF;
@@ -412,7 +425,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 
 template <int D, typename T>
 static hipError_t launch_bwd(const BwdParams& p, bool causal, hipStream_t st) {
-  const int64_t rows = (int64_t)p.B * p.Hq * p.S;
+  const int64_t rows = (int64_t)p.B * p.Hq * p.nst * 32;
   constexpr int RPB = 256 / (D / 8);
   const int64_t dblocks = (rows + RPB - 1) / RPB;
   hipLaunchKernelGGL((bwd_delta_kernel<T, D>), dim3((unsigned)(dblocks < 2048 ? dblocks : 2048)), dim3(256), 0, st,
@@ -534,7 +547,7 @@ using namespace nq;
 
 extern "C" int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S) {
   if (B <= 0 || Hq <= 0 || S <= 0) return 0;
-  return (int64_t)B * Hq * S * (int64_t)sizeof(float);
+  return (int64_t)B * Hq * ((S + 31) / 32) * 64 * (int64_t)sizeof(float);
 }
 
 extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -562,13 +575,14 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
       if ((strs[i][a] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "strides must be multiples of 16 bytes");
   }
   if (!lse) return nq_fail(NQ_ERR_INVALID, "the forward's LSE is required");
-  const int64_t need = (int64_t)B * Hq * S * (int64_t)sizeof(float);
+  const int64_t need = nq_attn_bwd_workspace_bytes(B, Hq, S);
   if (!workspace || workspace_bytes < need)
     return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
                    (long long)workspace_bytes);
   BwdParams p{};
   p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout; p.lse = lse;
-  p.delta = reinterpret_cast<float*>(workspace);
+  p.ws = reinterpret_cast<float*>(workspace);
+  p.nst = (S + 31) / 32;
   p.dq = dq; p.dk = dk; p.dv = dv;
   p.qsb = q_strides[0]; p.qsh = q_strides[1]; p.qss = q_strides[2];
   p.ksb = k_strides[0]; p.ksh = k_strides[1]; p.kss = k_strides[2];
