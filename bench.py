@@ -13,8 +13,10 @@ The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
 prefill kernel's own FLOPs by its average duration from HIP events recorded
 on its launch stream.  ``secondary`` holds the other workloads, each with its
-roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2).  ``cpu_baseline``
-times the oracle (fp32 torch on the host cores) on a bounded sample.
+roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs
+2.5x the forward's, the five matrix products of FlashAttention-2).
+``cpu_baseline`` times the oracle (fp32 torch on the host cores) on a bounded
+sample.
 """
 
 from __future__ import annotations
@@ -156,6 +158,46 @@ class Decode:
         return self.work / (step_ms * 1e-3) / 1e9, "GB/s"
 
 
+class Backward:
+    """FlashAttention-2 backward (delta + dQ + dK/dV kernels) of a causal prefill."""
+    kind = "backward"
+
+    def __init__(self, nq, name, B, S, Hq, Hkv, D, seed, device="cuda"):
+        self.nq, self.name = nq, name
+        self.B, self.S, self.Hq, self.Hkv, self.D = B, S, Hq, Hkv, D
+        # the attention's operands after QK-Norm + RoPE, in the projections' layout
+        self.q = _randn((B, S, Hq, D), seed, device).transpose(1, 2)
+        self.k = _randn((B, S, Hkv, D), seed + 100, device).transpose(1, 2)
+        self.v = _randn((B, S, Hkv, D), seed + 200, device).transpose(1, 2)
+        self.do = _randn((B, S, Hq, D), seed + 400, device).transpose(1, 2)
+        self.o, self.lse = nq.attention_prefill(self.q, self.k, self.v, causal=True, return_lse=True)
+        # FlashAttention-2 convention: 5 matrix products over the causal pairs
+        self.work = 2.5 * 4.0 * D * B * Hq * S * (S + 1) / 2
+        self.call = nq.ops.attention_backward(self.q, self.k, self.v, self.o, self.do, self.lse,
+                                              causal=True, plan=True)
+
+    def step(self, ev=None):
+        if ev is not None:
+            ev[0].record()
+        self.call.launch()
+        if ev is not None:
+            ev[1].record()
+
+    def describe(self):
+        return {"workload": self.name, "batch": self.B, "seq_len": self.S, "num_heads": self.Hq,
+                "num_kv_heads": self.Hkv, "head_dim": self.D, "causal": True}
+
+    def roofline(self, kernel_ms, traffic=None):
+        ach = self.work / (kernel_ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "kernel": "bwd_delta_kernel + bwd_dq_kernel + bwd_dkdv_kernel",
+                "kernel_ms": round(kernel_ms, 5)}
+
+    def throughput(self, step_ms):
+        return self.work / (step_ms * 1e-3) / 1e12, "TFLOP/s"
+
+
 def measured_traffic():
     """Per-launch HBM bytes (fetch + write) of the dominant kernels, as measured by
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and summarised in
@@ -231,8 +273,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workloads", default="c2,c3,c4,c5",
-                    help="comma list of c2 (headline), c3, c4, c5")
+    ap.add_argument("--workloads", default="c2,c3,c4,c5,c2_bwd,c3_bwd",
+                    help="comma list of c2 (headline), c3, c4, c5, c2_bwd, c3_bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 times), for scaling "
@@ -272,6 +314,12 @@ def main():
         if name == "c5":
             return Prefill(nq, "YaRN long-context prefill B1 S131072 Hq32 Hkv4 D128 causal bf16",
                            1, 131072, 32, 4, 128, seed=1004, rope_scaling=YARN, cpu_gen=False)
+        if name == "c2_bwd":
+            return Backward(nq, "Qwen3-1.7B-like attention backward B8 S2048 Hq16 Hkv8 D128 causal bf16",
+                            8, 2048, 16, 8, 128, seed=1005)
+        if name == "c3_bwd":
+            return Backward(nq, "Qwen3-8B-like attention backward B4 S8192 Hq32 Hkv8 D128 causal bf16",
+                            4, 8192, 32, 8, 128, seed=1006)
         raise SystemExit(f"unknown workload {name}")
 
     results = {}

@@ -15,6 +15,11 @@ Public surface, mirroring the reference:
   TextGenerator                eval/generate.py:20-183
   RingAttention, split_sequence   distributed/context_parallel.py:17-140 (one GPU's share)
 
+Training: ``Attention`` with autograd and ``flash_attention`` on tensors that
+require grad run the FlashAttention-2 backward kernels (``attention_backward``,
+``qk_norm_rope_backward``; autograd Functions ``attention_core`` and
+``flash_attention_train``) where the reference runs SDPA's autograd.
+
 Extensions with no reference counterpart: ``generate_greedy_batch`` (ragged
 batched greedy decoding against per-row cache lengths), ``PagedKVCache``
 (block-table page pool), ``attention_decode_paged`` (decode with the new
@@ -29,7 +34,8 @@ from .rope import RotaryEmbedding, apply_rotary_pos_emb, build_tables
 from .attention import Attention, KVCache, PagedKVCache, stats
 from .model import ModelConfig, Qwen3Model, TransformerBlock
 from .generate import TextGenerator, generate_greedy_batch
-from .ops import attention_merge_
+from .ops import attention_backward, attention_merge_, qk_norm_rope_backward
+from .autograd import attention_core, flash_attention_train
 from .ring import RingAttention, ring_attention_all_ranks, ring_schedule, ring_step, split_sequence
 
 __all__ = [
@@ -39,5 +45,6 @@ __all__ = [
     "ModelConfig", "Qwen3Model", "TransformerBlock", "TextGenerator", "generate_greedy_batch",
     "PagedKVCache", "attention_decode_paged", "kv_append_paged",
     "attention_merge_", "RingAttention", "ring_step", "ring_schedule", "split_sequence",
-    "ring_attention_all_ranks",
+    "ring_attention_all_ranks", "attention_backward", "qk_norm_rope_backward", "attention_core",
+    "flash_attention_train",
 ]

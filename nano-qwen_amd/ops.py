@@ -30,6 +30,8 @@ __all__ = [
     "attention_decode_paged",
     "kv_append_paged",
     "attention_merge_",
+    "attention_backward",
+    "qk_norm_rope_backward",
     "decode_workspace_bytes",
     "flash_attention",
     "apply_rope",
