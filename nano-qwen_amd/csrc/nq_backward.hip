@@ -290,8 +290,13 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r32 = lane & 31, hh = lane >> 5;
-  const int nkb = (p.T + BW_KEYS - 1) / BW_KEYS;
-  const int kblk = blockIdx.x % nkb, pair = blockIdx.x / nkb;
+  // key blocks in launch order across all (batch, kv head) pairs: under the
+  // causal mask the first keys see the most queries, so the heaviest blocks
+  // start first.  Consecutive blocks are different pairs: with a pair count
+  // that is a multiple of 8, a pair's blocks all land on one XCD (dispatch is
+  // round-robin over the 8) and share its L2 for the Q / dO stream.
+  const int npairs = p.B * p.Hkv;
+  const int kblk = blockIdx.x / npairs, pair = blockIdx.x % npairs;
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int k0 = kblk * BW_KEYS;
   const int key = k0 + wave * 32 + r32;  // this lane's key (C column)
@@ -302,15 +307,33 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
   const int qstart = CAUSAL ? max(0, k0 - p.coff) / BW_BQ * BW_BQ : 0;
   const int nqt = qstart < p.S ? (p.S - qstart + BW_BQ - 1) / BW_BQ : 0;
   const int niter = p.G * nqt;
+  // bf16 Q / dO tiles: this wave's DMA instruction i fills LDS bytes
+  // [(wave + 4i) * 1024, +1024), the lane's 16 bytes lying in tile row
+  // dr0 + i * DSTEP at the same swizzled chunk for every i (the swizzle
+  // repeats every 4 * 1024 bytes), so two lane constants cover the tile
+  constexpr int NPW = BW_BQ * L::RB / 1024 / 4;
+  constexpr int DSTEP = 4 * 1024 / L::RB;
+  static_assert(NPW >= 1 && (BW_BQ * L::RB) % 4096 == 0, "tile size");
+  const int dr0 = (wave * 1024 + lane * 16) / L::RB;
+  const int dlc = L::tsw(dr0, (lane * 16 % L::RB) / 16) * 8;
   auto stage = [&](int it, int buf) {
     const int g = it / nqt, qt = qstart + (it % nqt) * BW_BQ;
     const int head = kvh * p.G + g;
     unsigned char* base = smem + buf * BUF;
-    bw_tile<D, T, BW_BQ, true>(base, reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qt * p.qss,
-                               p.qss, p.S - qt, wave, lane);
-    bw_tile<D, T, BW_BQ, true>(base + TB,
-                               reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qt * p.doss,
-                               p.doss, p.S - qt, wave, lane);
+    const T* qsrc = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qt * p.qss;
+    const T* dsrc = reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qt * p.doss;
+    if constexpr (sizeof(T) == 2) {
+      const int last = p.S - qt - 1;  // rows past S clamp to the last row (masked)
+#pragma unroll
+      for (int i = 0; i < NPW; ++i) {
+        const int row = min(dr0 + i * DSTEP, last);
+        global_load_lds16(qsrc + (int64_t)row * p.qss + dlc, base + (wave + 4 * i) * 1024);
+        global_load_lds16(dsrc + (int64_t)row * p.doss + dlc, base + TB + (wave + 4 * i) * 1024);
+      }
+    } else {
+      bw_tile<D, T, BW_BQ, true>(base, qsrc, p.qss, p.S - qt, wave, lane);
+      bw_tile<D, T, BW_BQ, true>(base + TB, dsrc, p.doss, p.S - qt, wave, lane);
+    }
     // LSE (log2 units) and Delta of the tile's 32 rows: 256 contiguous bytes
     // of the scratch, one 16-byte piece per lane of the last wave's first 16
     if (wave == 3 && lane < 16)
@@ -372,27 +395,34 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
       s = mfma32(aq, kop[db], s);
       dp = mfma32(ad, bv, dp);
     }
-    // this lane's 16 query rows: hh*8 + 0..7 and 16 + hh*8 + 0..7, four at a time
-    floatx8 pv[2], ds[2];
+    // this lane's 16 query rows: hh*8 + 0..7 and 16 + hh*8 + 0..7, four at a
+    // time; P and dS go to bf16 (the B operands below) as soon as they exist
+    bf16x8 bpv[2], bdsv[2];
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int r0 = (i4 < 2 ? 0 : 16) + hh * 8 + (i4 & 1) * 4;
-      const floatx4 lv = *reinterpret_cast<const floatx4*>(lse_t + r0);
-      const floatx4 dv4 = *reinterpret_cast<const floatx4*>(dlt_t + r0);
+    for (int ks = 0; ks < 2; ++ks) {
+      floatx8 pv, ds;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i4 * 4 + u;
-        const int q = qt + r0 + u;
-        const bool keep = key < p.T && q < p.S && (!CAUSAL || key <= q + p.coff);
-        const float pe = fast_exp2(keep ? __builtin_fmaf(s[i], p.scale_log2, -lv[u]) : -INFINITY);
-        pv[i / 8][i % 8] = pe;
-        ds[i / 8][i % 8] = pe * (dp[i] - dv4[u]);
+      for (int i4h = 0; i4h < 2; ++i4h) {
+        const int r0 = ks * 16 + hh * 8 + i4h * 4;
+        const floatx4 lv = *reinterpret_cast<const floatx4*>(lse_t + r0);
+        const floatx4 dv4 = *reinterpret_cast<const floatx4*>(dlt_t + r0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = ks * 8 + i4h * 4 + u;
+          const int q = qt + r0 + u;
+          const bool keep = key < p.T && q < p.S && (!CAUSAL || key <= q + p.coff);
+          const float pe = fast_exp2(keep ? __builtin_fmaf(s[i], p.scale_log2, -lv[u]) : -INFINITY);
+          pv[i4h * 4 + u] = pe;
+          ds[i4h * 4 + u] = pe * (dp[i] - dv4[u]);
+        }
       }
+      bpv[ks] = to_bf16x8(pv);
+      bdsv[ks] = to_bf16x8(ds);
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 bp = to_bf16x8(pv[ks]);
-      const bf16x8 bds = to_bf16x8(ds[ks]);
+      const bf16x8 bp = bpv[ks];
+      const bf16x8 bds = bdsv[ks];
       bf16x8 ad[NDO], aq[NDO];
 #pragma unroll
       for (int dd = 0; dd < NDO; ++dd) {
