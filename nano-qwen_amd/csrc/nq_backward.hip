@@ -30,6 +30,8 @@
 // global_load_lds (one tile ahead), one barrier per tile; the transpose reads
 // are issued as inline asm so that the loads in flight are not waited for.
 
+#include <type_traits>
+
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
 
@@ -316,8 +318,8 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
   static_assert(NPW >= 1 && (BW_BQ * L::RB) % 4096 == 0, "tile size");
   const int dr0 = (wave * 1024 + lane * 16) / L::RB;
   const int dlc = L::tsw(dr0, (lane * 16 % L::RB) / 16) * 8;
-  auto stage = [&](int it, int buf) {
-    const int g = it / nqt, qt = qstart + (it % nqt) * BW_BQ;
+  // stage the (head g, query tile qt) step into buffer buf
+  auto stage = [&](int g, int qt, int buf) {
     const int head = kvh * p.G + g;
     unsigned char* base = smem + buf * BUF;
     const T* qsrc = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qt * p.qss;
@@ -339,6 +341,15 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
     if (wave == 3 && lane < 16)
       global_load_lds16(p.ws + bw_ws_index(p, b, head, qt) + lane * 4, base + 2 * TB);
   };
+  // steps run head by head, query tile by query tile
+  auto advance = [&](int& g, int& qt) {
+    qt += BW_BQ;
+    if (qt >= p.S) {
+      qt = qstart;
+      ++g;
+    }
+  };
+  int gn = 0, qtn = qstart;  // the next step to stage
   // V of the block's keys stays in LDS (read as the B operand of dP each
   // step); K of the lane's key is held in registers (B operand of S).  Both
   // stagings are waited for at the top of the first iteration (a workgroup
@@ -346,7 +357,8 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
   if (niter > 0) {
     bw_tile<D, T, BW_KEYS, false>(Vs, reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh + (int64_t)k0 * p.vss,
                                   p.vss, p.T - k0, wave, lane);
-    stage(0, 0);
+    stage(gn, qtn, 0);
+    advance(gn, qtn);
   }
 
   bf16x8 kop[NDB];
@@ -359,9 +371,12 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
   const int vrow_l = wave * 32 + r32;
   const int vrow_o = vrow_l * L::RB;
   const int prow = bw_perm32(r32);
-  int rro[NDB];
+  // Q / dO rows as the A operand of S^T / dP^T: chunk 2 db + hh of row
+  // prow.  The swizzle XORs chunk bits 2 and up, so chunks 4m + hh and
+  // 4m + 2 + hh lie 32 bytes apart: one offset per d-chunk pair
+  int rro[NDB / 2];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) rro[db] = prow * L::RB + L::tsw(prow, 2 * db + hh) * 16;
+  for (int m = 0; m < NDB / 2; ++m) rro[m] = prow * L::RB + L::tsw(prow, 4 * m + hh) * 16;
   int tro[NDO];
   {
     const int gi = lane >> 4, jj = lane & 15;
@@ -377,65 +392,106 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) dkacc[dd] = dvacc[dd] = floatx16{};
 
+  int qt = qstart;  // the current step's query tile
   for (int it = 0; it < niter; ++it) {
-    const int qt = qstart + (it % nqt) * BW_BQ;
     wait_vmcnt0();  // the LSE / Delta rows always come through global_load_lds
     __syncthreads();
-    if (it + 1 < niter) stage(it + 1, (it + 1) & 1);
+    if (it + 1 < niter) {
+      stage(gn, qtn, (it + 1) & 1);
+      advance(gn, qtn);
+    }
     const unsigned char* Qt = smem + (it & 1) * BUF;
     const unsigned char* Dt = Qt + TB;
     const float* lse_t = reinterpret_cast<const float*>(Qt + 2 * TB);
     const float* dlt_t = lse_t + BW_BQ;
+    // S^T and dP^T over the d chunks, the next chunk's three reads (Q, dO, V)
+    // in flight behind the current chunk's two MFMAs
+    const uint32_t qa = lds_addr(Qt), va = lds_addr(Vs) + vrow_o;
     floatx16 s = floatx16{}, dp = floatx16{};
+    bf16x8 aq[2], ad[2], bv[2];
+    auto rd_sdp = [&](int db, int slot) {
+      if (db & 1) {
+        aq[slot] = lds_read_b128_nowait<32>(qa + rro[db / 2]);
+        ad[slot] = lds_read_b128_nowait<TB + 32>(qa + rro[db / 2]);
+      } else {
+        aq[slot] = lds_read_b128_nowait<0>(qa + rro[db / 2]);
+        ad[slot] = lds_read_b128_nowait<TB>(qa + rro[db / 2]);
+      }
+      bv[slot] = lds_read_b128_nowait<0>(va + L::rsw(vrow_l, 2 * db + hh) * 16);
+    };
+    rd_sdp(0, 0);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(Qt + rro[db]);
-      const bf16x8 ad = *reinterpret_cast<const bf16x8*>(Dt + rro[db]);
-      const bf16x8 bv = *reinterpret_cast<const bf16x8*>(Vs + vrow_o + L::rsw(vrow_l, 2 * db + hh) * 16);
-      s = mfma32(aq, kop[db], s);
-      dp = mfma32(ad, bv, dp);
+      if (db + 1 < NDB) {
+        rd_sdp(db + 1, (db + 1) & 1);
+        lgkm_wait<3>();
+      } else {
+        lgkm_wait<0>();
+      }
+      s = mfma32(aq[db & 1], kop[db], s);
+      dp = mfma32(ad[db & 1], bv[db & 1], dp);
     }
     // this lane's 16 query rows: hh*8 + 0..7 and 16 + hh*8 + 0..7, four at a
-    // time; P and dS go to bf16 (the B operands below) as soon as they exist
+    // time; P and dS go to bf16 (the B operands below) as soon as they exist.
+    // A step whose 32 x 32 (key, query) square lies inside every bound skips
+    // the per-element mask (a wave-uniform test).
     bf16x8 bpv[2], bdsv[2];
+    auto probs = [&](auto masked) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      floatx8 pv, ds;
+      for (int ks = 0; ks < 2; ++ks) {
+        floatx8 pv, ds;
 #pragma unroll
-      for (int i4h = 0; i4h < 2; ++i4h) {
-        const int r0 = ks * 16 + hh * 8 + i4h * 4;
-        const floatx4 lv = *reinterpret_cast<const floatx4*>(lse_t + r0);
-        const floatx4 dv4 = *reinterpret_cast<const floatx4*>(dlt_t + r0);
+        for (int i4h = 0; i4h < 2; ++i4h) {
+          const int r0 = ks * 16 + hh * 8 + i4h * 4;
+          const floatx4 lv = *reinterpret_cast<const floatx4*>(lse_t + r0);
+          const floatx4 dv4 = *reinterpret_cast<const floatx4*>(dlt_t + r0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = ks * 8 + i4h * 4 + u;
-          const int q = qt + r0 + u;
-          const bool keep = key < p.T && q < p.S && (!CAUSAL || key <= q + p.coff);
-          const float pe = fast_exp2(keep ? __builtin_fmaf(s[i], p.scale_log2, -lv[u]) : -INFINITY);
-          pv[i4h * 4 + u] = pe;
-          ds[i4h * 4 + u] = pe * (dp[i] - dv4[u]);
+          for (int u = 0; u < 4; ++u) {
+            const int i = ks * 8 + i4h * 4 + u;
+            float x = __builtin_fmaf(s[i], p.scale_log2, -lv[u]);
+            if constexpr (decltype(masked)::value) {
+              // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
+              const int q = qt + r0 + u;
+              const bool keep = key < p.T && q < p.S && (!CAUSAL || key <= q + p.coff);
+              x = keep ? x : -INFINITY;
+            }
+            const float pe = fast_exp2(x);
+            pv[i4h * 4 + u] = pe;
+            ds[i4h * 4 + u] = pe * (dp[i] - dv4[u]);
+          }
         }
+        bpv[ks] = to_bf16x8(pv);
+        bdsv[ks] = to_bf16x8(ds);
       }
-      bpv[ks] = to_bf16x8(pv);
-      bdsv[ks] = to_bf16x8(ds);
+    };
+    const int kw1 = k0 + wave * 32 + 31;  // the wave's last key
+    if (kw1 < p.T && qt + BW_BQ <= p.S && (!CAUSAL || kw1 <= qt + p.coff))
+      probs(std::false_type{});
+    else
+      probs(std::true_type{});
+    // dV += dO^T P^T and dK += Q^T dS^T, one (16-query step ks, 32-wide d
+    // block dd) at a time, the next pair's transpose reads in flight
+    bf16x8 td[2], tq[2];
+    auto rd_t = [&](int t, int slot) {
+      const int ks = t / NDO, dd = t % NDO;
+      td[slot] = bw_tr8<D>(Dt + tro[dd] + ks * 16 * L::RB);
+      tq[slot] = bw_tr8<D>(Qt + tro[dd] + ks * 16 * L::RB);
+    };
+    rd_t(0, 0);
+#pragma unroll
+    for (int t = 0; t < 2 * NDO; ++t) {
+      if (t + 1 < 2 * NDO) {
+        rd_t(t + 1, (t + 1) & 1);
+        lgkm_wait<4>();
+      } else {
+        lgkm_wait<0>();
+      }
+      const int ks = t / NDO, dd = t % NDO;
+      dvacc[dd] = mfma32(td[t & 1], bpv[ks], dvacc[dd]);
+      dkacc[dd] = mfma32(tq[t & 1], bdsv[ks], dkacc[dd]);
     }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 bp = bpv[ks];
-      const bf16x8 bds = bdsv[ks];
-      bf16x8 ad[NDO], aq[NDO];
-#pragma unroll
-      for (int dd = 0; dd < NDO; ++dd) {
-        ad[dd] = bw_tr8<D>(Dt + tro[dd] + ks * 16 * L::RB);
-        aq[dd] = bw_tr8<D>(Qt + tro[dd] + ks * 16 * L::RB);
-      }
-      lgkm_wait<0>();
-#pragma unroll
-      for (int dd = 0; dd < NDO; ++dd) {
-        dvacc[dd] = mfma32(ad[dd], bp, dvacc[dd]);
-        dkacc[dd] = mfma32(aq[dd], bds, dkacc[dd]);
-      }
-    }
+    int gdummy = 0;
+    advance(gdummy, qt);
   }
 
   if (key >= p.T) return;
@@ -604,6 +660,10 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
     for (int a = 0; a < 3; ++a)
       if ((strs[i][a] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "strides must be multiples of 16 bytes");
   }
+  // the dK/dV kernel addresses a 32-row query tile with 32-bit lane offsets
+  for (const int64_t rs : {q_strides[2], do_strides[2]})
+    if (rs < 0 || rs * esz * 32 >= (int64_t(1) << 31))
+      return nq_fail(NQ_ERR_UNSUPPORTED, "q and dout position strides must lie in [0, 2^26 / element size)");
   if (!lse) return nq_fail(NQ_ERR_INVALID, "the forward's LSE is required");
   const int64_t need = nq_attn_bwd_workspace_bytes(B, Hq, S);
   if (!workspace || workspace_bytes < need)

@@ -110,6 +110,13 @@ __device__ __forceinline__ shortx4 lds_read_tr4_nowait(uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
   return r;
 }
+// A plain 16-byte LDS read issued the same way (waited for with lgkm_wait).
+template <int OFF>
+__device__ __forceinline__ bf16x8 lds_read_b128_nowait(uint32_t addr) {
+  bf16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
 // rows r0..r0+3 at addr and r0+4..r0+7 at addr + HI bytes, as one operand
 template <int HI>
 __device__ __forceinline__ bf16x8 lds_read_tr8_nowait(uint32_t addr) {
