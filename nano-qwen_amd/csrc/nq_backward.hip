@@ -235,36 +235,69 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
     __syncthreads();
     if (j + 1 < ntiles) stage(j + 1, (j + 1) & 1);
     const unsigned char* Kt = smem + (j & 1) * 2 * TB;
-    const unsigned char* Vt = Kt + TB;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    const uint32_t ka = lds_addr(Kt);  // the V tile is TB bytes on
+    // a tile inside every row's bounds (all keys below T and at or before
+    // the block's first query's frontier, no rows past S) skips the mask
+    const bool full = n0 + BW_BN <= p.T && q0 + p.BM <= p.S && (!CAUSAL || n0 + BW_BN - 1 <= q0 + p.coff);
+    // the two 32-key blocks of the tile (kb a compile-time constant, so its
+    // LDS offset goes into the read instructions)
+    auto key_block = [&](auto KB) {
+      constexpr int kb = decltype(KB)::value;
+      // S^T and dP^T over the d chunks, the next chunk's K and V reads in
+      // flight behind the current chunk's two MFMAs
       floatx16 s = floatx16{}, dp = floatx16{};
+      bf16x8 ak[2], av[2];
+      auto rd_sdp = [&](int db, int slot) {
+        ak[slot] = lds_read_b128_nowait<kb * 32 * L::RB>(ka + kro[db]);
+        av[slot] = lds_read_b128_nowait<TB + kb * 32 * L::RB>(ka + vro[db]);
+      };
+      rd_sdp(0, 0);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const bf16x8 ak = *reinterpret_cast<const bf16x8*>(Kt + kro[db] + kb * 32 * L::RB);
-        const bf16x8 av = *reinterpret_cast<const bf16x8*>(Vt + vro[db] + kb * 32 * L::RB);
-        s = mfma32(ak, qop[db], s);
-        dp = mfma32(av, dop[db], dp);
+        if (db + 1 < NDB) {
+          rd_sdp(db + 1, (db + 1) & 1);
+          lgkm_wait<2>();
+        } else {
+          lgkm_wait<0>();
+        }
+        s = mfma32(ak[db & 1], qop[db], s);
+        dp = mfma32(av[db & 1], dop[db], dp);
       }
-      floatx8 ds[2];
+      bf16x8 bds[2];
+      auto grads = [&](auto masked) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = n0 + kb * 32 + bw_cidx(i, hh);
-        // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
-        const float pe = fast_exp2(key <= lim ? __builtin_fmaf(s[i], p.scale_log2, -lse2) : -INFINITY);
-        ds[i / 8][i % 8] = pe * (dp[i] - dlt);
-      }
+        for (int ks = 0; ks < 2; ++ks) {
+          floatx8 ds;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = ks * 8 + e;
+            float x = __builtin_fmaf(s[i], p.scale_log2, -lse2);
+            if constexpr (decltype(masked)::value) {
+              // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
+              const int key = n0 + kb * 32 + bw_cidx(i, hh);
+              x = key <= lim ? x : -INFINITY;
+            }
+            ds[e] = fast_exp2(x) * (dp[i] - dlt);
+          }
+          bds[ks] = to_bf16x8(ds);
+        }
+      };
+      if (full)
+        grads(std::false_type{});
+      else
+        grads(std::true_type{});
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 bds = to_bf16x8(ds[ks]);
-        bf16x8 ak[NDO];
+        bf16x8 akt[NDO];
 #pragma unroll
-        for (int dd = 0; dd < NDO; ++dd) ak[dd] = bw_tr8<D>(Kt + kto[dd] + (kb * 32 + ks * 16) * L::RB);
+        for (int dd = 0; dd < NDO; ++dd) akt[dd] = bw_tr8<D>(Kt + kto[dd] + (kb * 32 + ks * 16) * L::RB);
         lgkm_wait<0>();
 #pragma unroll
-        for (int dd = 0; dd < NDO; ++dd) dqacc[dd] = mfma32(ak[dd], bds, dqacc[dd]);
+        for (int dd = 0; dd < NDO; ++dd) dqacc[dd] = mfma32(akt[dd], bds[ks], dqacc[dd]);
       }
-    }
+    };
+    key_block(std::integral_constant<int, 0>{});
+    key_block(std::integral_constant<int, 1>{});
   }
 
   if (!qvalid) return;
