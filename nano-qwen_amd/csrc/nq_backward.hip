@@ -425,14 +425,23 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) dkacc[dd] = dvacc[dd] = floatx16{};
 
-  int qt = qstart;  // the current step's query tile
+  int qnext = qstart;
   for (int it = 0; it < niter; ++it) {
+    const int qt = qnext;  // this step's query tile
+    {
+      int g_unused = 0;
+      advance(g_unused, qnext);
+    }
     wait_vmcnt0();  // the LSE / Delta rows always come through global_load_lds
     __syncthreads();
     if (it + 1 < niter) {
       stage(gn, qtn, (it + 1) & 1);
       advance(gn, qtn);
     }
+    // a wave whose keys all lie past T, or (causal) after every query of the
+    // step, has P = 0 there: nothing to add
+    const int kw0 = k0 + wave * 32;
+    if (kw0 >= p.T || (CAUSAL && kw0 > qt + BW_BQ - 1 + p.coff)) continue;
     const unsigned char* Qt = smem + (it & 1) * BUF;
     const unsigned char* Dt = Qt + TB;
     const float* lse_t = reinterpret_cast<const float*>(Qt + 2 * TB);
@@ -497,7 +506,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
         bdsv[ks] = to_bf16x8(ds);
       }
     };
-    const int kw1 = k0 + wave * 32 + 31;  // the wave's last key
+    const int kw1 = kw0 + 31;  // the wave's last key
     if (kw1 < p.T && qt + BW_BQ <= p.S && (!CAUSAL || kw1 <= qt + p.coff))
       probs(std::false_type{});
     else
@@ -523,8 +532,6 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
       dvacc[dd] = mfma32(td[t & 1], bpv[ks], dvacc[dd]);
       dkacc[dd] = mfma32(tq[t & 1], bdsv[ks], dkacc[dd]);
     }
-    int gdummy = 0;
-    advance(gdummy, qt);
   }
 
   if (key >= p.T) return;
