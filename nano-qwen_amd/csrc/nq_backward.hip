@@ -61,6 +61,7 @@ struct BwdParams {
 constexpr int BW_BN = 64;     // keys per tile (dQ kernel)
 constexpr int BW_BQ = 32;     // query rows per tile (dK/dV kernel)
 constexpr int BW_KEYS = 128;  // keys per dK/dV workgroup (32 per wave)
+constexpr int64_t BW_DQ_WIDE_MIN_WGS = 2048;  // 8-wave dQ workgroups needed to prefer them
 
 __device__ __forceinline__ int bw_perm32(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 // C element i of a lane in half hh -> index (key or query) within its 32-block
@@ -120,14 +121,14 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
 // [m*1024, m*1024+1024), lane t the 16 bytes at +16t, so the lane loads the
 // logical chunk that belongs in that physical slot (the swizzle is an XOR,
 // its own inverse).  fp32 storage: loads converted in registers.
-template <int D, typename T, int NR, bool TSW>
+template <int D, typename T, int NR, bool TSW, int NW = 4>
 __device__ __forceinline__ void bw_tile(unsigned char* tile, const T* src, int64_t rs, int nvalid, int wave,
                                         int lane) {
   using L = BwTile<D>;
   if constexpr (sizeof(T) == 2) {
     constexpr int NI = NR * L::RB / 1024;
-    static_assert(NI % 4 == 0 || NI < 4, "tile size");
-    for (int m = wave; m < NI; m += 4) {
+    static_assert(NI % NW == 0 || NI < NW, "tile size");
+    for (int m = wave; m < NI; m += NW) {
       const int pbyte = m * 1024 + lane * 16;
       const int r = pbyte / L::RB, pc = (pbyte % L::RB) / 16;
       const int lc = TSW ? L::tsw(r, pc) : L::rsw(r, pc);
@@ -136,7 +137,7 @@ __device__ __forceinline__ void bw_tile(unsigned char* tile, const T* src, int64
     }
   } else {
     constexpr int CH = NR * L::CPR;
-    for (int c = threadIdx.x; c < CH; c += 256) {
+    for (int c = threadIdx.x; c < CH; c += 64 * NW) {
       const int r = c / L::CPR, ch = c % L::CPR;
       const int row = r < nvalid ? r : nvalid - 1;
       const bf16x8 val = to_bf16x8(Vec8<T>::load_f32(src + (int64_t)row * rs + ch * 8));
@@ -153,8 +154,8 @@ __device__ __forceinline__ bf16x8 bw_tr8(const unsigned char* p) {
 }
 
 // ---------------------------------------------------------------- dQ
-template <int D, typename T, bool CAUSAL>
-__global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
+template <int D, typename T, bool CAUSAL, int NW>
+__global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
   using L = BwTile<D>;
   constexpr int NDB = D / 16, NDO = D / 32;
   constexpr int TB = BW_BN * L::RB;
@@ -175,8 +176,9 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdParams p) {
   const T* vb0 = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
   auto stage = [&](int j, int buf) {
     const int n0 = j * BW_BN;
-    bw_tile<D, T, BW_BN, true>(smem + buf * 2 * TB, kb0 + (int64_t)n0 * p.kss, p.kss, p.T - n0, wave, lane);
-    bw_tile<D, T, BW_BN, false>(smem + buf * 2 * TB + TB, vb0 + (int64_t)n0 * p.vss, p.vss, p.T - n0, wave, lane);
+    bw_tile<D, T, BW_BN, true, NW>(smem + buf * 2 * TB, kb0 + (int64_t)n0 * p.kss, p.kss, p.T - n0, wave, lane);
+    bw_tile<D, T, BW_BN, false, NW>(smem + buf * 2 * TB + TB, vb0 + (int64_t)n0 * p.vss, p.vss, p.T - n0, wave,
+                                    lane);
   };
   stage(0, 0);  // its latency overlaps the Q / dO loads below
 
@@ -550,7 +552,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
 }
 
 template <int D, typename T>
-static hipError_t launch_bwd(const BwdParams& p, bool causal, hipStream_t st) {
+static hipError_t launch_bwd(const BwdParams& p, int nw, bool causal, hipStream_t st) {
   const int64_t rows = (int64_t)p.B * p.Hq * p.nst * 32;
   constexpr int RPB = 256 / (D / 8);
   const int64_t dblocks = (rows + RPB - 1) / RPB;
@@ -560,11 +562,14 @@ static hipError_t launch_bwd(const BwdParams& p, bool causal, hipStream_t st) {
   if (e != hipSuccess) return e;
   const dim3 gq((unsigned)(p.nqb * p.B * p.Hkv));
   const dim3 gk((unsigned)(((p.T + BW_KEYS - 1) / BW_KEYS) * p.B * p.Hkv));
+  const dim3 bq(64 * nw);
   if (causal) {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, T, true>), gq, dim3(256), 0, st, p);
+    if (nw == 8) hipLaunchKernelGGL((bwd_dq_kernel<D, T, true, 8>), gq, bq, 0, st, p);
+    else hipLaunchKernelGGL((bwd_dq_kernel<D, T, true, 4>), gq, bq, 0, st, p);
     hipLaunchKernelGGL((bwd_dkdv_kernel<D, T, true>), gk, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, T, false>), gq, dim3(256), 0, st, p);
+    if (nw == 8) hipLaunchKernelGGL((bwd_dq_kernel<D, T, false, 8>), gq, bq, 0, st, p);
+    else hipLaunchKernelGGL((bwd_dq_kernel<D, T, false, 4>), gq, bq, 0, st, p);
     hipLaunchKernelGGL((bwd_dkdv_kernel<D, T, false>), gk, dim3(256), 0, st, p);
   }
   return hipGetLastError();
@@ -723,7 +728,11 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   p.dksb = dk_strides[0]; p.dksh = dk_strides[1]; p.dkss = dk_strides[2];
   p.dvsb = dv_strides[0]; p.dvsh = dv_strides[1]; p.dvss = dv_strides[2];
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
-  p.BM = 128 / G;
+  // dQ workgroups: 8 waves (256 query rows: each K/V tile load serves twice
+  // the rows) when that still gives enough workgroups to fill the device
+  const int64_t wide_wgs = (int64_t)B * Hkv * ((S + 256 / G - 1) / (256 / G));
+  const int nw = wide_wgs >= BW_DQ_WIDE_MIN_WGS ? 8 : 4;
+  p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
   p.coff = T - S;
   p.scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
@@ -731,9 +740,9 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NQ_DTYPE_BF16)
-    e = D == 128 ? launch_bwd<128, bf16>(p, causal != 0, st) : launch_bwd<64, bf16>(p, causal != 0, st);
+    e = D == 128 ? launch_bwd<128, bf16>(p, nw, causal != 0, st) : launch_bwd<64, bf16>(p, nw, causal != 0, st);
   else
-    e = D == 128 ? launch_bwd<128, float>(p, causal != 0, st) : launch_bwd<64, float>(p, causal != 0, st);
+    e = D == 128 ? launch_bwd<128, float>(p, nw, causal != 0, st) : launch_bwd<64, float>(p, nw, causal != 0, st);
   return nq_check_launch(e);
 }
 

@@ -185,3 +185,28 @@ def test_module_training_gradients_against_oracle(dtype):
             f"grad {n}: mean error {float(e_k.mean()):.3e}, reference bf16 autograd {float(e_r.mean()):.3e}"
         assert float(e_k.max()) <= 1.5 * float(e_r.max()) + floor, \
             f"grad {n}: max error {float(e_k.max()):.3e}, reference bf16 autograd {float(e_r.max()):.3e}"
+
+
+def test_attention_backward_wide_dq_workgroups_bit_equal():
+    """B8 S4096 16/8 D128 causal: enough dQ work for the 8-wave (256-row) workgroups.
+    Each row's dQ accumulates over the same key tiles in the same order in the 4-wave
+    workgroups that a one-sequence launch uses, and tiles past a row's frontier add
+    exact zeros, so the batched call equals the per-sequence calls bit for bit."""
+    say("bwd wide dQ workgroups vs per-sequence launches")
+    B, Hq, Hkv, S, D = 8, 16, 8, 4096, 128
+    q = randn(B, S, Hq, D, seed=561, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    k = randn(B, S, Hkv, D, seed=562, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    v = randn(B, S, Hkv, D, seed=563, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    do = randn(B, S, Hq, D, seed=564, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    o, lse = ops.attention_prefill(q, k, v, causal=True, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q, k, v, o, do, lse, causal=True)
+    for b in (0, 5):
+        sl = slice(b, b + 1)
+        dq1, dk1, dv1 = ops.attention_backward(q[sl], k[sl], v[sl], o[sl], do[sl], lse[sl], causal=True)
+        for got, ref, name in ((dq[sl], dq1, "dq"), (dk[sl], dk1, "dk"), (dv[sl], dv1, "dv")):
+            assert torch.equal(got, ref), f"{name} batch {b}: max diff {float((got.float() - ref.float()).abs().max())}"
+    # and one sequence against fp64 autograd on its last 256 queries (all keys)
+    b, q0 = 3, S - 256
+    qs = q[b:b + 1, :, q0:].cpu()
+    _, rq, _, _ = _ref_grads(qs, k[b:b + 1].cpu(), v[b:b + 1].cpu(), do[b:b + 1, :, q0:].cpu(), True)
+    _close_rel(dq[b:b + 1, :, q0:], rq, "dq (wide workgroups, last 256 rows)")
