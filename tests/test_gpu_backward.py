@@ -94,6 +94,23 @@ def test_attention_backward_long_sequence():
     _close_rel(dv, rv, "dv S=2048")
 
 
+@pytest.mark.parametrize("S,T", [(100, 333), (257, 64)])
+def test_attention_backward_non_causal_cross_lengths(S, T):
+    """Non-causal with S != T (more keys than queries and fewer), ragged sizes."""
+    say(f"bwd non-causal S={S} T={T}")
+    B, Hq, Hkv, D = 2, 8, 2, 128
+    q = randn(B, Hq, S, D, seed=571, dtype=torch.bfloat16)
+    k = randn(B, Hkv, T, D, seed=572, dtype=torch.bfloat16)
+    v = randn(B, Hkv, T, D, seed=573, dtype=torch.bfloat16)
+    do = randn(B, Hq, S, D, seed=574, dtype=torch.bfloat16)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=False, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=False)
+    _, rq, rk, rv = _ref_grads(q, k, v, do, False)
+    _close_rel(dq, rq, "dq")
+    _close_rel(dk, rk, "dk")
+    _close_rel(dv, rv, "dv")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("D", [64, 128])
 def test_norm_rope_backward_against_fp64_autograd(dtype, D):

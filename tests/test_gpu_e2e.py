@@ -225,3 +225,41 @@ def test_fixed_semantics_cache_matches_nocache(gold, model):
         model.set_cache_semantics(False)
     torch.testing.assert_close(pre.float(), full[:-1].float(), atol=0.05, rtol=0)
     torch.testing.assert_close(dec.float(), full[-1].float(), atol=0.05, rtol=0)
+
+
+def test_training_step_gradients_against_oracle(weights):
+    """One cross-entropy training step of the fp32 model on the kernels (attention
+    forward and backward: prefill with LSE, the FlashAttention-2 backward, the
+    QK-Norm + RoPE backward), every parameter gradient against fp64 autograd
+    through the oracle model.  Gate per tensor, relative to its largest reference
+    magnitude: max-abs <= 2e-2 and mean-abs <= 2e-3 (the products run on bf16
+    MFMA)."""
+    say("training step gradients (kernels vs oracle fp64 autograd)")
+    torch.manual_seed(0)
+    m = Qwen3Model(ModelConfig(**MODEL)).train()
+    m.load_state_dict(weights, strict=True)
+    m = m.to("cuda")
+    g = torch.Generator().manual_seed(601)
+    ids = torch.randint(0, MODEL["vocab_size"], (2, 96), generator=g)
+    before = stats["kernel_train_forward"]
+    out = m(ids.cuda(), labels=ids.cuda())
+    out["loss"].backward()
+    assert stats["kernel_train_forward"] == before + MODEL["num_hidden_layers"]
+
+    ref_w = {n: t.detach().double().clone().requires_grad_(True) for n, t in weights.items()}
+    logits = model_forward(ref_w, MODEL, ids)
+    loss = torch.nn.functional.cross_entropy(logits[:, :-1].reshape(-1, logits.shape[-1]),
+                                             ids[:, 1:].reshape(-1))
+    loss.backward()
+    got_loss, ref_loss = out["loss"].detach().item(), loss.detach().item()
+    assert abs(got_loss - ref_loss) <= 1e-2 * ref_loss, (got_loss, ref_loss)
+    grads = dict(m.named_parameters())
+    for name, ref in ref_w.items():
+        got = grads[name].grad
+        assert got is not None, name
+        got = got.double().cpu()
+        r = ref.grad
+        scale = float(r.abs().max())
+        d = (got - r).abs()
+        assert float(d.max()) <= 2e-2 * scale and float(d.mean()) <= 2e-3 * scale, \
+            f"{name}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {scale:.3e})"
