@@ -414,7 +414,7 @@ prefill_kernel(PrefillParams p) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      va = vn;
+      if (idx + 1 < NPV) va = vn;
     }
     if (NEXT) mx_cur = xor32_max(mxn) * p.scale_log2;
   };
