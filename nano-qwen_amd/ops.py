@@ -15,7 +15,6 @@ drop-in ``Attention`` module are ``qk_norm_rope``, ``attention_prefill`` and
 from __future__ import annotations
 
 import ctypes
-import math
 from typing import Optional, Tuple
 
 import torch

@@ -1,13 +1,11 @@
 """GPU parity of the prefill attention kernel against the oracle (fp32 reference math)."""
 
-import math
-
 import pytest
 import torch
 
 import nano_qwen_amd as nq
 from oracle import attention, attention_path, rms_norm, rope_tables, rotate_half
-from tests.helpers import BF16_MAX_ABS, BF16_MEAN_ABS, assert_bf16_close, err_stats, randn, say
+from tests.helpers import assert_bf16_close, randn, say
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
