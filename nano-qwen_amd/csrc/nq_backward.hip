@@ -315,8 +315,9 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------- dK, dV
+// D = 64 fits three workgroups per CU (168 VGPRs), D = 128 two
 template <int D, typename T, bool CAUSAL>
-__global__ void __launch_bounds__(256, 2) bwd_dkdv_kernel(BwdParams p) {
+__global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParams p) {
   using L = BwTile<D>;
   constexpr int NDB = D / 16, NDO = D / 32;
   constexpr int TB = BW_BQ * L::RB;
