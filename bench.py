@@ -211,7 +211,8 @@ def measured_traffic():
         if len(f) != 6 or line.startswith("#") or f[0] == "kernel":
             continue
         kern, w, fetch_mb, write_mb = f[0], f[1], float(f[4]), float(f[5])
-        if kern in ("prefill_kernel", "decode_stream_kernel", "decode_merge_kernel"):
+        if kern in ("prefill_kernel", "decode_stream_kernel", "decode_merge_kernel",
+                    "bwd_delta_kernel", "bwd_dq_kernel", "bwd_dkdv_kernel"):
             out[w] = out.get(w, 0.0) + (fetch_mb + write_mb) * 1e6
     return {w: int(b) for w, b in out.items()}
 
