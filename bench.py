@@ -190,7 +190,7 @@ class Backward:
         ach = self.work / (kernel_ms * 1e-3) / 1e12
         return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                "kernel": "bwd_delta_kernel + bwd_dq_kernel + bwd_dkdv_kernel",
+                "kernel": "bwd_dq_kernel + bwd_dkdv_kernel",
                 "kernel_ms": round(kernel_ms, 5)}
 
     def throughput(self, step_ms):

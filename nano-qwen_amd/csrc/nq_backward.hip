@@ -11,11 +11,12 @@
 //   P = exp(scale * Q K^T - LSE),  Delta = rowsum(dO * O),
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - Delta),
 //   dQ = scale * dS K,  dK = scale * dS^T Q.
-// Three kernels: Delta (one row per D/8 lanes); dQ per query block (the
-// forward's decomposition: a workgroup owns the G heads x BM positions of one
-// kv head and walks the key tiles); dK/dV per key block (a workgroup owns 128
-// keys of one kv head and walks every query row of its G heads, so the GQA sum
-// over heads happens in registers, with no atomics).
+// Two kernels: dQ per query block (the forward's decomposition: a workgroup
+// owns the G heads x BM positions of one kv head and walks the key tiles; it
+// also forms each row's Delta and stores it with the row's LSE for the next
+// kernel); dK/dV per key block (a workgroup owns 128 keys of one kv head and
+// walks every query row of its G heads, so the GQA sum over heads happens in
+// registers, with no atomics).
 //
 // MFMA layouts (v_mfma_f32_32x32x16_bf16): A lane l holds row l%32, k = 8*(l/32)..+7;
 // B lane l holds column l%32, the same k; C lane l holds column l%32, rows
@@ -44,7 +45,7 @@ struct BwdParams {
   const void* o;
   const void* dout;
   const float* lse;  // (B, Hq, S) natural log
-  // scratch written by bwd_delta_kernel: per (batch, head) and 32-row query
+  // scratch written by bwd_dq_kernel: per (batch, head) and 32-row query
   // tile, 64 floats = [32 x LSE * log2(e) | 32 x Delta], rows past S zero
   float* ws;
   int nst;           // 32-row tiles per (batch, head)
@@ -78,41 +79,10 @@ struct BwTile {
   __device__ static int tsw(int r, int c) { return c ^ (4 * ((r / RPL) & (D / 32 - 1))); }
 };
 
-// ---------------------------------------------------------------- Delta
+// ---------------------------------------------------------------- scratch
 // Index of (batch b, head h, query s) in the scratch: its LSE; Delta is 32 on.
 __device__ __forceinline__ int64_t bw_ws_index(const BwdParams& p, int b, int h, int s) {
   return (((int64_t)b * p.Hq + h) * p.nst + s / 32) * 64 + (s & 31);
-}
-
-template <typename T, int D>
-__global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
-  constexpr int LPR = D / 8;
-  constexpr int RPB = 256 / LPR;
-  const int sub = threadIdx.x % LPR;
-  const int SP = p.nst * 32;  // padded rows per (batch, head)
-  const int64_t nrows = (int64_t)p.B * p.Hq * SP;
-  for (int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; row < nrows; row += (int64_t)gridDim.x * RPB) {
-    const int s = (int)(row % SP);
-    const int h = (int)((row / SP) % p.Hq);
-    const int b = (int)(row / ((int64_t)SP * p.Hq));
-    float acc = 0.f, l2 = 0.f;
-    if (s < p.S) {
-      const floatx8 o =
-          Vec8<T>::load_f32(reinterpret_cast<const T*>(p.o) + b * p.osb + h * p.osh + s * p.oss + sub * 8);
-      const floatx8 d =
-          Vec8<T>::load_f32(reinterpret_cast<const T*>(p.dout) + b * p.dosb + h * p.dosh + s * p.doss + sub * 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(o[e], d[e], acc);
-#pragma unroll
-      for (int m = 1; m < LPR; m <<= 1) acc += shfl_xor_f(acc, m);
-      l2 = p.lse[((int64_t)b * p.Hq + h) * p.S + s] * kLog2e;
-    }
-    if (sub == 0) {
-      const int64_t w = bw_ws_index(p, b, h, s);
-      p.ws[w] = l2;
-      p.ws[w + 32] = acc;
-    }
-  }
 }
 
 // Stage a tile of NR rows (rows >= nvalid clamp to the last valid row; their
@@ -189,19 +159,46 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
   const bool qvalid = qi < p.S;
   const int qi_c = qvalid ? qi : p.S - 1;
 
+  // the row's Q and dO (B operands), and Delta = rowsum(dO * O): the two
+  // lanes of a row (hh = 0, 1) each hold half of it
   bf16x8 qop[NDB], dop[NDB];
+  float dlt;
   {
     const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qi_c * p.qss;
     const T* drow = reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qi_c * p.doss;
+    const T* orow = reinterpret_cast<const T*>(p.o) + b * p.osb + head * p.osh + (int64_t)qi_c * p.oss;
+    float acc = 0.f;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       qop[db] = to_bf16x8(Vec8<T>::load_f32(qrow + db * 16 + hh * 8));
-      dop[db] = to_bf16x8(Vec8<T>::load_f32(drow + db * 16 + hh * 8));
+      const floatx8 d = Vec8<T>::load_f32(drow + db * 16 + hh * 8);
+      const floatx8 o = Vec8<T>::load_f32(orow + db * 16 + hh * 8);
+      dop[db] = to_bf16x8(d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(o[e], d[e], acc);
+    }
+    dlt = xor32_sum(acc);
+  }
+  const float lse2 = p.lse[((int64_t)b * p.Hq + head) * p.S + qi_c] * kLog2e;
+  // the dK/dV kernel reads both per 32-row tile from the scratch; the
+  // workgroup of the last q-block also zeroes its heads' slots past S (the
+  // dK/dV kernel's masked rows then see finite values)
+  if (qvalid && hh == 0) {
+    const int64_t wi = bw_ws_index(p, b, head, qi);
+    p.ws[wi] = lse2;
+    p.ws[wi + 32] = dlt;
+  }
+  if (qblk == p.nqb - 1) {
+    const int pad = p.nst * 32 - p.S;  // 0..31 slots per head
+    for (int t = threadIdx.x; t < p.G * 32; t += 64 * NW) {
+      const int g2 = t / 32, s2 = p.S + t % 32;
+      if (t % 32 < pad) {
+        const int64_t w2 = bw_ws_index(p, b, kvh * p.G + g2, s2);
+        p.ws[w2] = 0.f;
+        p.ws[w2 + 32] = 0.f;
+      }
     }
   }
-  const int64_t wi = bw_ws_index(p, b, head, qi_c);
-  const float lse2 = p.ws[wi];
-  const float dlt = p.ws[wi + 32];
 
   // LDS offsets: K / V rows through the key permutation (A of S^T and dP^T);
   // K^T through transpose reads (A of dQ^T)
@@ -554,13 +551,6 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
 
 template <int D, typename T>
 static hipError_t launch_bwd(const BwdParams& p, int nw, bool causal, hipStream_t st) {
-  const int64_t rows = (int64_t)p.B * p.Hq * p.nst * 32;
-  constexpr int RPB = 256 / (D / 8);
-  const int64_t dblocks = (rows + RPB - 1) / RPB;
-  hipLaunchKernelGGL((bwd_delta_kernel<T, D>), dim3((unsigned)(dblocks < 2048 ? dblocks : 2048)), dim3(256), 0, st,
-                     p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   const dim3 gq((unsigned)(p.nqb * p.B * p.Hkv));
   const dim3 gk((unsigned)(((p.T + BW_KEYS - 1) / BW_KEYS) * p.B * p.Hkv));
   const dim3 bq(64 * nw);
