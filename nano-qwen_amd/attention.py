@@ -335,6 +335,10 @@ class Attention(nn.Module):
         q = self.q_proj(hidden_states)
         k = self.k_proj(hidden_states)
         v = self.v_proj(hidden_states)
+        if B == 0 or S == 0:
+            # no query rows: the reference's SDPA returns an empty output and its
+            # cache update appends nothing (attention.py:103-118); no launch here
+            return self.o_proj(q.new_zeros(B, S, H * D))
         dropout = self.training and getattr(self.config, "attention_dropout", 0.0) > 0
         qw = self.q_norm.weight if self.qk_norm else None
         kw = self.k_norm.weight if self.qk_norm else None

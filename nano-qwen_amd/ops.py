@@ -629,10 +629,12 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
     Returns a contiguous (B, H, N, D) tensor.
     """
     _require_device(q, k, v)
+    if q.numel() == 0:
+        # no query rows: an empty output, as the reference's grid of zero blocks gives
+        return torch.empty_like(q, memory_format=torch.contiguous_format)
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
         from .autograd import flash_attention_train
         return flash_attention_train(q, k, v, causal=causal, sm_scale=sm_scale)
-    B, H, N, D = q.shape
     out = torch.empty_like(q, memory_format=torch.contiguous_format)
     return attention_prefill(q, k, v, causal=causal, sm_scale=sm_scale, out=out)
 

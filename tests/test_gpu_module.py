@@ -139,3 +139,21 @@ def test_opt_in_cache_positions_equal_full_causal_prefill():
     for t in range(5, h.shape[1]):
         outs.append(attn(h[:, t:t + 1], kv_cache=cache))
     assert_bf16_close(torch.cat(outs, 1), full, "decode loop vs full", max_abs=3e-2)
+
+
+@torch.no_grad()
+def test_empty_inputs_give_empty_outputs():
+    """Zero batch rows or zero tokens: empty outputs (as the reference's SDPA), the cache
+    untouched, no kernel launched."""
+    say("module empty inputs")
+    attn, h = _module()
+    before = dict(nq.stats)
+    for shape in ((0, 5, h.shape[-1]), (h.shape[0], 0, h.shape[-1])):
+        out = attn(h.new_zeros(shape))
+        assert tuple(out.shape) == shape
+    cache = nq.KVCache()
+    out = attn(h[:, :0], kv_cache=cache)
+    assert out.shape[1] == 0 and cache.seq_len == 0
+    assert nq.stats == before
+    q = torch.zeros(2, 4, 0, 64, device=DEV, dtype=torch.bfloat16)
+    assert nq.flash_attention(q, q, q).shape == q.shape
