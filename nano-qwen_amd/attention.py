@@ -133,14 +133,14 @@ class KVCache:
 
     def _spare_lens(self) -> torch.Tensor:
         """The second lengths buffer: a fused decode step writes lens + 1 into it."""
-        if getattr(self, "_lens_spare", None) is None:
+        if self._lens_spare is None:
             self._lens_spare = torch.empty_like(self.lens)
         return self._lens_spare
 
     def _identity_table(self) -> torch.Tensor:
         """Block table [[0], [1], ...]: row b of the storage is page b."""
         B = self._k.shape[0]
-        t = getattr(self, "_ident", None)
+        t = self._ident
         if t is None or t.shape[0] != B or t.device != self._k.device:
             t = torch.arange(B, dtype=torch.int32, device=self._k.device).view(B, 1)
             self._ident = t
