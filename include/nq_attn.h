@@ -221,7 +221,11 @@ int nq_attn_merge(void* o, const int64_t* o_strides, float* lse, const void* o_p
                   const int64_t* part_strides, const float* lse_part, int B, int H, int S, int D,
                   int dtype, void* stream);
 
-/* Bytes of fp32 workspace nq_attn_bwd needs (the per-row Delta = rowsum(dO * O)). */
+/*
+ * Bytes of fp32 workspace nq_attn_bwd needs: per query row, the forward's LSE
+ * (in log2 units) and Delta = rowsum(dO * O), both formed by its first kernel
+ * and read by its second.
+ */
 int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S);
 
 /*
