@@ -134,3 +134,13 @@ def test_kvcache_host_semantics_match_concatenation():
     assert cache.seq_len == 78 and cache.capacity >= 78
     cache.reset()
     assert cache.seq_len == 0 and cache.key.shape[2] == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message before any GPU work."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
