@@ -89,7 +89,8 @@ def test_decode_equals_last_row_of_prefill():
 
 
 def test_qwen3_235b_decode_full_size():
-    """B64, Hq64/Hkv4, D128, lens ~ U[1024, 32768], T_cap 32768; tails poisoned with NaN."""
+    """B64, Hq64/Hkv4, D128, lens ~ U[1024, 32768], T_cap 32768; tails poisoned with NaN;
+    every row against the oracle."""
     say("decode Qwen3-235B-A22B B64 T_cap 32768")
     B, Hq, Hkv, D, Tcap = 64, 64, 4, 128, 32768
     g = torch.Generator().manual_seed(1003)
@@ -106,8 +107,7 @@ def test_qwen3_235b_decode_full_size():
     o = nq.attention_decode(q.to(DEV), kc, vc, ld, max_len=int(lens.max()), cos=cos.to(DEV),
                             sin=sin.to(DEV)).cpu()
     assert torch.isfinite(o.float()).all()
-    picks = [int(lens.argmin()), int(lens.argmax()), 0, 17, 42, 63]
-    for b in picks:
+    for b in range(B):  # every row, the shortest and the longest among them
         L = int(lens[b])
         ref = decode_path(q[b:b + 1].float(), kc[b:b + 1, :, :L].float().cpu(),
                           vc[b:b + 1, :, :L].float().cpu(), lens[b:b + 1], q_weight=None,

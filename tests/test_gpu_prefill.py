@@ -129,19 +129,28 @@ def test_explicit_position_ids_and_yarn_high_positions():
 
 
 def test_qwen3_1p7b_like_full_size():
-    """B8 S2048 Hq16 Hkv8 D128 bf16; oracle on batches 0 and 7 (all heads, all rows)."""
+    """B8 S2048 Hq16 Hkv8 D128 bf16: CPU oracle on batches 0 and 7 (all heads, all rows),
+    and every row of every head of every batch row against the fp32 math on the device."""
     say("prefill Qwen3-1.7B-like B8 S2048")
     B, S, Hq, Hkv, D = 8, 2048, 16, 8, 128
+    G = Hq // Hkv
     q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=1001)
     cos, sin = rope_tables(D, S, 1e6)
-    o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
-                      cos.to(DEV), sin.to(DEV)).cpu()
+    od = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
+                       cos.to(DEV), sin.to(DEV))
+    o = od.cpu()
     assert torch.isfinite(o.float()).all()
     for b in (0, 7):
         ref = attention_path(q[b:b + 1].float(), k[b:b + 1].float(), v[b:b + 1].float(),
                              q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin,
                              q_pos=torch.arange(S), causal=True)
         assert_bf16_close(o[b:b + 1], ref, f"1.7B b={b}")
+    for b in range(B):
+        for kvh in range(Hkv):
+            refs = _fp32_blocks_on_device(q, k, v, qw, kw, cos, sin, kvh, G, [0, 1024], 1024, b=b)
+            for r0, ref in zip([0, 1024], refs):
+                assert_bf16_close(od[b, kvh * G:(kvh + 1) * G, r0:r0 + 1024], ref,
+                                  f"1.7B b={b} kvh={kvh} rows={r0}")
 
 
 def _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows):
@@ -158,22 +167,32 @@ def _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows):
 
 
 def test_qwen3_8b_like_full_size():
-    """B4 S8192 Hq32 Hkv8 D128 bf16; oracle on sampled 128-row blocks."""
+    """B4 S8192 Hq32 Hkv8 D128 bf16: CPU oracle on sampled 128-row blocks of two (batch,
+    kv head) pairs, and every head of every batch row on 1024-row blocks (the first, the
+    last and two seeded random ones) against the fp32 math on the device."""
     say("prefill Qwen3-8B-like B4 S8192")
     B, S, Hq, Hkv, D = 4, 8192, 32, 8, 128
     G = Hq // Hkv
     q, k, v, qw, kw = make(B, S, Hq, Hkv, D, torch.bfloat16, seed=1002)
     cos, sin = rope_tables(D, S, 1e6)
     o = gpu_attention(q.to(DEV), k.to(DEV), v.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6,
-                      cos.to(DEV), sin.to(DEV)).cpu()
+                      cos.to(DEV), sin.to(DEV))
     rows = [(0, 128), (4000, 4128), (S - 128, S)]
     for b, kvh in ((0, 0), (3, 7)):
         for (r0, r1), ref in zip(rows, _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows)):
             assert_bf16_close(o[b:b + 1, kvh * G:(kvh + 1) * G, r0:r1], ref, f"8B b={b} kvh={kvh} rows={r0}")
+    n = 1024
+    gen = torch.Generator().manual_seed(1006)
+    starts = [0, S - n] + torch.randint(1, S - n, (2,), generator=gen).tolist()
+    for b in range(B):
+        for kvh in range(Hkv):
+            refs = _fp32_blocks_on_device(q, k, v, qw, kw, cos, sin, kvh, G, starts, n, b=b)
+            for r0, ref in zip(starts, refs):
+                assert_bf16_close(o[b, kvh * G:(kvh + 1) * G, r0:r0 + n], ref, f"8B b={b} kvh={kvh} rows={r0}")
 
 
-def _fp32_blocks_on_device(q, k, v, qw, kw, cos, sin, kvh, G, starts, n):
-    """Causal rows [r0, r0 + n) of batch 0, the G heads of kv head kvh, in fp32 on the device.
+def _fp32_blocks_on_device(q, k, v, qw, kw, cos, sin, kvh, G, starts, n, b=0):
+    """Causal rows [r0, r0 + n) of batch b, the G heads of kv head kvh, in fp32 on the device.
 
     The oracle's composition (rms_norm, rotate_half, softmax(q k^T / sqrt(D)) v, all in
     fp32 from the bf16-valued inputs), with the two products as fp32 torch matmuls on the
@@ -182,12 +201,12 @@ def _fp32_blocks_on_device(q, k, v, qw, kw, cos, sin, kvh, G, starts, n):
     """
     D = q.shape[-1]
     cd, sd = cos.to(DEV), sin.to(DEV)
-    kh = rotate_half(rms_norm(k[0, kvh].to(DEV).float(), kw.to(DEV), 1e-6), cd, sd)
-    vd = v[0, kvh].to(DEV).float()
+    kh = rotate_half(rms_norm(k[b, kvh].to(DEV).float(), kw.to(DEV), 1e-6), cd, sd)
+    vd = v[b, kvh].to(DEV).float()
     outs = []
     for r0 in starts:
         r1 = r0 + n
-        qs = q[0, kvh * G:(kvh + 1) * G, r0:r1].to(DEV).float()
+        qs = q[b, kvh * G:(kvh + 1) * G, r0:r1].to(DEV).float()
         qh = rotate_half(rms_norm(qs, qw.to(DEV), 1e-6), cd[r0:r1], sd[r0:r1])
         sc = torch.matmul(qh, kh[:r1].t().contiguous()) * (D ** -0.5)
         past = torch.arange(r1, device=DEV)[None, :] > torch.arange(r0, r1, device=DEV)[:, None]
