@@ -227,3 +227,59 @@ def test_attention_backward_wide_dq_workgroups_bit_equal():
     qs = q[b:b + 1, :, q0:].cpu()
     _, rq, _, _ = _ref_grads(qs, k[b:b + 1].cpu(), v[b:b + 1].cpu(), do[b:b + 1, :, q0:].cpu(), True)
     _close_rel(dq[b:b + 1, :, q0:], rq, "dq (wide workgroups, last 256 rows)")
+
+
+def _fp32_grads_on_device(q, k, v, do, causal=True):
+    """fp32 autograd on the device for one (batch, kv head) slice.
+
+    q, do: (G, S, D); k, v: (T, D).  The oracle's math (softmax(q k^T / sqrt(D)) v, key j
+    kept for query i iff j <= i + T - S) with fp32 torch matmuls on the GPU, for shapes
+    where fp64 autograd on the CPU would take minutes.  Returns dq, dk, dv in fp32.
+    """
+    qd, kd, vd = (t.detach().to(DEV).float().requires_grad_(True) for t in (q, k, v))
+    S, T, D = qd.shape[1], kd.shape[0], qd.shape[2]
+    sc = torch.matmul(qd, kd.t().contiguous()) * D ** -0.5
+    if causal:
+        past = torch.arange(T, device=DEV)[None, :] > torch.arange(S, device=DEV)[:, None] + (T - S)
+        sc = sc.masked_fill(past, float("-inf"))
+    o = torch.matmul(torch.softmax(sc, dim=-1), vd)
+    o.backward(do.to(DEV).float())
+    return qd.grad, kd.grad, vd.grad
+
+
+def test_device_fp32_gradients_match_fp64_autograd():
+    """The device reference of the full-size backward test against fp64 autograd on the CPU."""
+    say("bwd device fp32 reference vs fp64 autograd")
+    G, S, T, D = 4, 300, 333, 128
+    q = randn(1, G, S, D, seed=571, dtype=torch.bfloat16)
+    k = randn(1, 1, T, D, seed=572, dtype=torch.bfloat16)
+    v = randn(1, 1, T, D, seed=573, dtype=torch.bfloat16)
+    do = randn(1, G, S, D, seed=574, dtype=torch.bfloat16)
+    for causal in (True, False):
+        _, rq, rk, rv = _ref_grads(q, k, v, do, causal)
+        gq, gk, gv = _fp32_grads_on_device(q[0], k[0, 0], v[0, 0], do[0], causal)
+        for got, ref, name in ((gq, rq[0], "dq"), (gk, rk[0, 0], "dk"), (gv, rv[0, 0], "dv")):
+            torch.testing.assert_close(got.double().cpu(), ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()),
+                                       msg=lambda m: f"{name} causal={causal}: {m}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(8, 16, 8, 2048), (4, 32, 8, 8192)])
+def test_attention_backward_full_size(B, Hq, Hkv, S):
+    """The two benchmarked backward shapes (Qwen3-1.7B-like and 8B-like, D128 causal bf16)
+    in one launch each; every (batch, kv head) slice's dq, dk, dv against fp32 autograd on
+    the device."""
+    say(f"bwd full size B{B} S{S} {Hq}/{Hkv}")
+    D, G = 128, Hq // Hkv
+    q = randn(B, S, Hq, D, seed=581, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    k = randn(B, S, Hkv, D, seed=582, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    v = randn(B, S, Hkv, D, seed=583, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    do = randn(B, S, Hq, D, seed=584, dtype=torch.bfloat16).to(DEV).transpose(1, 2)
+    o, lse = ops.attention_prefill(q, k, v, causal=True, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q, k, v, o, do, lse, causal=True)
+    torch.cuda.synchronize()
+    for b in range(B):
+        for kvh in range(Hkv):
+            hs = slice(kvh * G, (kvh + 1) * G)
+            rq, rk, rv = _fp32_grads_on_device(q[b, hs], k[b, kvh], v[b, kvh], do[b, hs])
+            for got, ref, name in ((dq[b, hs], rq, "dq"), (dk[b, kvh], rk, "dk"), (dv[b, kvh], rv, "dv")):
+                _close_rel(got, ref, f"{name} b={b} kvh={kvh}")
