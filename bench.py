@@ -7,7 +7,8 @@ seeded inputs already resident in HBM:
   prefill  K-Norm + RoPE row kernel (K-hat), then the fused prefill kernel
            (Q-Norm + RoPE on load, causal GQA FlashAttention forward);
   decode   append of the new token's K-hat/V into the cache, then the decode
-           kernel (a persistent grid streaming the ragged cache) and its merge.
+           kernel (a persistent grid streaming the ragged cache) and its merge;
+           the paged form fuses the append into the decode launch.
 The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 (B8 S2048 Hq16 Hkv8 D128 causal bf16); FLOPs are the algorithmic
 4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
@@ -157,8 +158,57 @@ class Decode:
         return self.work / (step_ms * 1e-3) / 1e9, "GB/s"
 
 
+class PagedDecode(Decode):
+    """The same decode against a paged pool, with the append fused into the decode launch.
+
+    64-row pages are dealt to the sequences in a seeded random order.  Sequence b holds
+    lens[b] - 1 keys; the launch norms, rotates and writes the new token's K (and V) at row
+    lens[b] - 1 and attends all lens[b] keys, so the bytes match the dense workload's.
+    """
+
+    def __init__(self, nq, name, B, Hq, Hkv, D, Tcap, seed, page=64, device="cuda"):
+        self.nq, self.name, self.page = nq, name, page
+        self.B, self.Hq, self.Hkv, self.D, self.Tcap = B, Hq, Hkv, D, Tcap
+        g = torch.Generator().manual_seed(seed)
+        self.lens_cpu = torch.randint(1024, Tcap + 1, (B,), generator=g, dtype=torch.int32)
+        self.held = (self.lens_cpu - 1).to(device)           # keys before the new token
+        self.lens_out = torch.empty(B, dtype=torch.int32, device=device)
+        self.max_len = int(self.lens_cpu.max())
+        npp = Tcap // page
+        self.bt = torch.randperm(B * npp, generator=g).view(B, npp).to(torch.int32).to(device)
+        gd = torch.Generator(device=device).manual_seed(seed)
+        self.kp = torch.randn(B * npp, Hkv, page, D, generator=gd, device=device, dtype=torch.bfloat16)
+        self.vp = torch.randn(B * npp, Hkv, page, D, generator=gd, device=device, dtype=torch.bfloat16)
+        self.q = _randn((B, Hq, 1, D), seed + 1, device)
+        self.knew = _randn((B, Hkv, 1, D), seed + 2, device)
+        self.vnew = _randn((B, Hkv, 1, D), seed + 3, device)
+        self.w = torch.ones(D, device=device)
+        cos, sin = nq.build_tables(D, Tcap, 1e6)
+        self.cos, self.sin = cos.to(device), sin.to(device)
+        self.out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
+        nbytes = nq.decode_workspace_bytes(B, Hq, Hkv, D, self.max_len)
+        self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        self.work = float(2 * Hkv * D * 2 * int(self.lens_cpu.sum()) + 2 * B * Hq * D * 2)
+        self.d_call = nq.attention_decode_paged(
+            self.q, self.kp, self.vp, self.bt, self.held, max_len=self.max_len, k_new=self.knew,
+            v_new=self.vnew, k_weight=self.w, lens_out=self.lens_out, q_weight=self.w, eps=1e-6,
+            cos=self.cos, sin=self.sin, out=self.out, workspace=self.ws, plan=True)
+
+    def step(self, ev=None):
+        if ev is not None:
+            ev[0].record()
+        self.d_call.launch()
+        if ev is not None:
+            ev[1].record()
+
+    def describe(self):
+        d = super().describe()
+        d["cache"] = f"paged, {self.page}-row pages in a seeded random order, append fused"
+        return d
+
+
 class Backward:
-    """FlashAttention-2 backward (delta + dQ + dK/dV kernels) of a causal prefill."""
+    """FlashAttention-2 backward (dQ kernel, which also forms Delta, then dK/dV) of a causal prefill."""
     kind = "backward"
 
     def __init__(self, nq, name, B, S, Hq, Hkv, D, seed, device="cuda"):
@@ -212,7 +262,7 @@ def measured_traffic():
             continue
         kern, w, fetch_mb, write_mb = f[0], f[1], float(f[4]), float(f[5])
         if kern in ("prefill_kernel", "decode_stream_kernel", "decode_merge_kernel",
-                    "bwd_delta_kernel", "bwd_dq_kernel", "bwd_dkdv_kernel"):
+                    "bwd_dq_kernel", "bwd_dkdv_kernel"):
             out[w] = out.get(w, 0.0) + (fetch_mb + write_mb) * 1e6
     return {w: int(b) for w, b in out.items()}
 
@@ -273,8 +323,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workloads", default="c2,c3,c4,c5,c2_bwd,c3_bwd",
-                    help="comma list of c2 (headline), c3, c4, c5, c2_bwd, c3_bwd")
+    ap.add_argument("--workloads", default="c2,c3,c4,c4_paged,c5,c2_bwd,c3_bwd",
+                    help="comma list of c2 (headline), c3, c4, c4_paged, c5, c2_bwd, c3_bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 times), for scaling "
@@ -311,6 +361,9 @@ def main():
         if name == "c4":
             return Decode(nq, "Qwen3-235B-A22B decode B64 Hq64 Hkv4 D128, ragged KV cache bf16",
                           64, 64, 4, 128, 32768, seed=1003)
+        if name == "c4_paged":
+            return PagedDecode(nq, "Qwen3-235B-A22B decode B64 Hq64 Hkv4 D128, paged KV cache bf16, "
+                               "fused K/V append", 64, 64, 4, 128, 32768, seed=1003)
         if name == "c5":
             return Prefill(nq, "YaRN long-context prefill B1 S131072 Hq32 Hkv4 D128 causal bf16",
                            1, 131072, 32, 4, 128, seed=1004, rope_scaling=YARN, cpu_gen=False)

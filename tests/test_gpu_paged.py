@@ -289,3 +289,55 @@ def test_generate_greedy_batch_paged_equals_dense():
     dense, _ = nq.generate_greedy_batch(m, prompts, 40)
     paged, _ = nq.generate_greedy_batch(m, prompts, 40, page_size=32)
     assert paged == dense
+
+
+def test_fused_append_paged_full_size():
+    """The 235B-like decode (B64, Hq64/Hkv4, D128, lengths U[1024, 32768]) on a pool of
+    64-row pages dealt in a seeded random order, with the append fused: every row against
+    the oracle, and every appended K-hat/V row equal to the row kernel's.  Rows past each
+    sequence's keys, the appended row included, start as NaN."""
+    say("fused append paged B64 64/4 T_cap 32768")
+    B, Hq, Hkv, D, Tcap, P = 64, 64, 4, 128, 32768, 64
+    g = torch.Generator().manual_seed(1003)
+    lens = torch.randint(1024, Tcap + 1, (B,), generator=g, dtype=torch.int32)
+    held = lens - 1                                   # keys before the new token
+    npp = Tcap // P
+    bt = torch.randperm(B * npp, generator=g).view(B, npp).to(torch.int32)
+    gd = torch.Generator(device=DEV).manual_seed(1003)
+    kp = torch.randn(B * npp, Hkv, P, D, generator=gd, device=DEV, dtype=torch.bfloat16)
+    vp = torch.randn(B * npp, Hkv, P, D, generator=gd, device=DEV, dtype=torch.bfloat16)
+    for b in range(B):
+        h = int(held[b])
+        j0 = h // P
+        for pool in (kp, vp):
+            pool[int(bt[b, j0]), :, h - j0 * P:] = float("nan")
+            pool[bt[b, j0 + 1:].long().to(DEV)] = float("nan")
+    q = randn(B, Hq, D, seed=1011, dtype=torch.bfloat16)
+    kn = randn(B, Hkv, D, seed=1012, dtype=torch.bfloat16)
+    vn = randn(B, Hkv, D, seed=1013, dtype=torch.bfloat16)
+    qw = 1 + 0.02 * randn(D, seed=1014)
+    kw = 1 + 0.02 * randn(D, seed=1015)
+    cos, sin = rope_tables(D, Tcap, 1e6)
+    dv = lambda t: t.to(DEV)  # noqa: E731
+    lens_out = torch.empty(B, dtype=torch.int32, device=DEV)
+    o = nq.attention_decode_paged(dv(q), kp, vp, dv(bt), dv(held), max_len=int(lens.max()),
+                                  k_new=dv(kn), v_new=dv(vn), k_weight=dv(kw), lens_out=lens_out,
+                                  q_weight=dv(qw), eps=1e-6, cos=dv(cos), sin=dv(sin)).cpu()
+    assert lens_out.cpu().tolist() == lens.tolist()
+    assert torch.isfinite(o.float()).all()
+    # the row kernel's K-hat / V rows of the new tokens, at each sequence's query position
+    kref = torch.empty(B, Hkv, 1, D, dtype=torch.bfloat16, device=DEV)
+    vref = torch.empty_like(kref)
+    ops.qk_norm_rope(k=dv(kn)[:, :, None], v=dv(vn)[:, :, None], k_out=kref, v_out=vref,
+                     k_weight=dv(kw), eps=1e-6, cos=dv(cos), sin=dv(sin),
+                     position_ids=dv(held)[:, None])
+    for b in range(B):
+        L = int(lens[b])
+        ids = bt[b, :-(-L // P)].long().to(DEV)
+        kd = kp[ids].permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :L].cpu()
+        vd = vp[ids].permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :L].cpu()
+        assert torch.equal(kd[:, L - 1], kref[b, :, 0].cpu()), f"appended K-hat row, b={b}"
+        assert torch.equal(vd[:, L - 1], vref[b, :, 0].cpu()), f"appended V row, b={b}"
+        ref = _oracle_append(q[b:b + 1], kn[b:b + 1], vn[b:b + 1], kd[None], vd[None], held[b:b + 1],
+                             qw, kw, cos, sin, held[b:b + 1])
+        assert_bf16_close(o[b:b + 1], ref, f"fused append paged b={b} len={L}")
