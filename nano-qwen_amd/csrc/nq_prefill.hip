@@ -311,9 +311,10 @@ prefill_kernel(PrefillParams p) {
   // interleaved with the exp/sum/convert of P[j] (sched_barrier keeps them
   // interleaved, since a wave issues in order); then O += V[j]^T P[j] with the
   // masking and row max of S[j+1] interleaved into those MFMAs.
-  auto step = [&](auto parity, auto has_next, int j) {
+  auto step = [&](auto parity, auto has_next, auto may_mask, int j) {
     constexpr int P = decltype(parity)::value;       // == j & 1
     constexpr bool NEXT = decltype(has_next)::value;  // j + 1 < ntiles
+    constexpr bool MASKN = decltype(may_mask)::value; // tile j + 1 may need masking
     floatx16* s_cur = P ? sB : sA;
     floatx16* s_next = P ? sA : sB;
     const int n0 = j * PF_BN;
@@ -391,7 +392,7 @@ prefill_kernel(PrefillParams p) {
     auto vread = [&](int idx) {
       return lds_read_tr8_nowait<8 * D>(Vt + v_off[idx % NDO] + (idx / NDO) * 16 * Tl::ROW_BYTES);
     };
-    if (NEXT) mask_tile(s_next, n0 + PF_BN);  // diagonal / last tiles only
+    if (NEXT && MASKN) mask_tile(s_next, n0 + PF_BN);  // diagonal / last tiles only
     constexpr int NPV = 4 * NDO;        // PV MFMAs
     constexpr int MPER = 32 / NPV;      // S[j+1] elements folded into the max per MFMA
     float mxn = -INFINITY;
@@ -423,16 +424,25 @@ prefill_kernel(PrefillParams p) {
   using I1 = std::integral_constant<int, 1>;
   using Yes = std::integral_constant<bool, true>;
   using No = std::integral_constant<bool, false>;
+  // Tiles below jfree lie inside T and before every row's causal frontier, so a
+  // step whose next tile is one of them carries no mask branch.  That branch would
+  // split the step into basic blocks, and the compiler would then sink the exp2
+  // work of P[j] below the S[j+1] MFMAs it is meant to interleave with.
+  const int jfree = min(ntiles, min(p.T / PF_BN, CAUSAL ? (q0 + coff + 1) / PF_BN : ntiles));
   int j = 0;
+  for (; j + 2 < jfree; j += 2) {
+    step(I0{}, Yes{}, No{}, j);
+    step(I1{}, Yes{}, No{}, j + 1);
+  }
   for (; j + 2 < ntiles; j += 2) {
-    step(I0{}, Yes{}, j);
-    step(I1{}, Yes{}, j + 1);
+    step(I0{}, Yes{}, Yes{}, j);
+    step(I1{}, Yes{}, Yes{}, j + 1);
   }
   if (ntiles - j == 2) {
-    step(I0{}, Yes{}, j);
-    step(I1{}, No{}, j + 1);
+    step(I0{}, Yes{}, Yes{}, j);
+    step(I1{}, No{}, Yes{}, j + 1);
   } else {
-    step(I0{}, No{}, j);
+    step(I0{}, No{}, Yes{}, j);
   }
 
   l_i = xor32_sum(l_i);
