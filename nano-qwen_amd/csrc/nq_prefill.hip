@@ -309,8 +309,9 @@ prefill_kernel(PrefillParams p) {
   // against the row max of S[j] (found in the previous step); then one
   // branch-free block in which the MFMAs of S[j+1] = K[j+1] Q^T are
   // interleaved with the exp/sum/convert of P[j] (sched_barrier keeps them
-  // interleaved, since a wave issues in order); then O += V[j]^T P[j] with the
-  // masking and row max of S[j+1] interleaved into those MFMAs.
+  // interleaved, since a wave issues in order); then, in the steps that may need
+  // it, the mask of S[j+1]; then O += V[j]^T P[j], with the row max of S[j+1]
+  // taken alongside those MFMAs.
   auto step = [&](auto parity, auto has_next, auto may_mask, int j) {
     constexpr int P = decltype(parity)::value;       // == j & 1
     constexpr bool NEXT = decltype(has_next)::value;  // j + 1 < ntiles
