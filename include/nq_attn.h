@@ -14,11 +14,16 @@
  *   - dtype codes: NQ_DTYPE_BF16 (bfloat16 stored as 16-bit words) or
  *     NQ_DTYPE_F32.  Matrix products run on bf16 MFMA with fp32 accumulation;
  *     norm, RoPE and softmax arithmetic is fp32.
- *   - head_dim must be 64 or 128.  num_heads % num_kv_heads == 0 and query head
- *     h reads kv head h / (num_heads / num_kv_heads).
+ *   - head_dim must be 32, 64 or 128 (the reference's configs use 32 and 128;
+ *     kernels/flash_attn.py:106 also allows 16 and 256, which are refused
+ *     here with NQ_ERR_UNSUPPORTED).  num_heads % num_kv_heads == 0 and query
+ *     head h reads kv head h / (num_heads / num_kv_heads).
  *   - cos/sin tables are fp32 (max_pos, head_dim/2) row-major, as built by the
- *     reference's RotaryEmbedding (plain RoPE or YaRN).  Positions outside
- *     [0, max_pos) are clamped into the table.
+ *     reference's RotaryEmbedding (plain RoPE or YaRN).  A row rotated at a
+ *     position outside [0, max_pos) comes out NaN (the reference's table
+ *     lookup, model/rope.py:123-129, fails there; positions held on the
+ *     device cannot be reported from a kernel, so callers that know them on
+ *     the host check them there).
  *   - Return value: NQ_OK (0) on success, a positive NQ_ERR_* code for an
  *     argument error, or a negative value -(hipError_t) for a launch error.
  *     nq_last_error() returns a thread-local message for the last failure.
@@ -78,6 +83,19 @@ int nq_qk_norm_rope(const void* q, const int64_t* q_strides, void* q_out,
                     const int32_t* kv_row_base, int kv_row0, void* stream);
 
 /*
+ * RMSNorm over rows of `width` elements (a multiple of 8): the forward of
+ * model/norm.py:11-22 (RMSNorm, used as QK-Norm at model/attention.py:95-97
+ * and as the layer norms of model/transformer.py), with its cast order and
+ * dtype promotion: y = (x * rsqrt(mean(x^2) + eps)) rounded to x's dtype, times
+ * weight, stored in the promoted dtype of x and weight (bf16 only when both
+ * are bf16; dtype_y must be that dtype).  x and y are `rows` rows with the
+ * given row strides (elements); weight has `width` contiguous elements.
+ */
+int nq_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, void* y,
+               int64_t y_row_stride, int64_t rows, int width, int dtype_x, int dtype_w,
+               int dtype_y, float eps, void* stream);
+
+/*
  * Causal / full GQA prefill attention (FlashAttention-2 style forward).
  *
  * Replaces kernels/flash_attn.py:130-143 (flash_attention) and the
@@ -128,8 +146,9 @@ int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int max_le
  *
  * q: (B, Hq, D) with strides {batch, head}; k_cache/v_cache: (B, Hkv, T_cap, D)
  *   with strides {batch, head, seq}, holding post-norm post-RoPE K and raw V.
- * lens: int32 (B), 1 <= lens[b] <= max_len <= T_cap (the kernel clamps to
- *   max_len); NULL = every row has max_len keys.
+ * lens: int32 (B), 0 <= lens[b] <= max_len <= T_cap; NULL = every row has
+ *   max_len keys.  A row with no keys gets zeros; a row whose lens[b] lies
+ *   outside [0, max_len] attends nothing and gets NaN.
  * q_pos: int32 (B) RoPE positions of the query token; NULL = q_pos0 for
  *   every row, or lens[b] - 1 when q_pos0 < 0.
  * o: output (B, Hq, D) with strides {batch, head}.
@@ -170,6 +189,8 @@ int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const void* k_ca
  *   lens[b] of the cache (its page must be mapped), and attended together with
  *   keys [0, lens[b]).  The query position is q_pos[b], else q_pos0, else
  *   lens[b].  lens_out (may be NULL; must not alias lens) receives lens + 1.
+ *   A sequence whose lens[b] + 1 exceeds max_len (or lens[b] < 0) appends
+ *   nothing, keeps lens_out[b] = lens[b] and gets NaN output.
  *   Calls that overlap on one sequence race; a single call is race-free.
  * max_len bounds the keys attended per sequence (the appended one included)
  *   and sizes the workspace (nq_attn_decode_workspace_bytes); bt_stride must

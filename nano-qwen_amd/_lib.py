@@ -44,6 +44,11 @@ SIGNATURES = {
         _p, _i32,                      # kv_row_base, kv_row0
         _p,                            # stream
     ]),
+    "nq_rmsnorm": (_i32, [
+        _p, _i64, _p, _p, _i64,                      # x, x_row_stride, weight, y, y_row_stride
+        _i64, _i32, _i32, _i32, _i32,                # rows, width, dtype_x, dtype_w, dtype_y
+        _f32, _p,                                    # eps, stream
+    ]),
     "nq_attn_prefill_fwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,  # q, k, v, o (+ strides)
         _p,                                          # lse

@@ -77,6 +77,11 @@ class KVCache:
         self.lens: Optional[torch.Tensor] = None
         self._lens_spare: Optional[torch.Tensor] = None
         self._ident: Optional[torch.Tensor] = None
+        # device copy of seq_len for every row, kept by the fused one-token
+        # step (which writes lens + 1 into the spare); valid while _dev_at == seq_len
+        self._dev_lens: Optional[torch.Tensor] = None
+        self._dev_spare: Optional[torch.Tensor] = None
+        self._dev_at = -1
 
     @property
     def seq_len(self) -> int:
@@ -137,6 +142,26 @@ class KVCache:
             self._lens_spare = torch.empty_like(self.lens)
         return self._lens_spare
 
+    def _step_lengths(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(lens, lens_next) for a fused one-token step of an unragged cache:
+        lens holds seq_len for every row (refilled only when it went stale, e.g.
+        after a prefill or update()); the step writes seq_len + 1 to lens_next."""
+        B = self._k.shape[0]
+        if self._dev_lens is None or self._dev_lens.shape[0] != B or self._dev_lens.device != self._k.device:
+            self._dev_lens = torch.empty(B, dtype=torch.int32, device=self._k.device)
+            self._dev_spare = torch.empty_like(self._dev_lens)
+            self._dev_at = -1
+        if self._dev_at != self._len:
+            self._dev_lens.fill_(self._len)
+            self._dev_at = self._len
+        return self._dev_lens, self._dev_spare
+
+    def _step_done(self) -> None:
+        """After a fused one-token step: the spare holds the new lengths."""
+        self._dev_lens, self._dev_spare = self._dev_spare, self._dev_lens
+        self.advance(1)
+        self._dev_at = self._len
+
     def _identity_table(self) -> torch.Tensor:
         """Block table [[0], [1], ...]: row b of the storage is page b."""
         B = self._k.shape[0]
@@ -162,6 +187,7 @@ class KVCache:
         self._len = 0
         self.lens = None
         self._lens_spare = None
+        self._dev_at = -1
         self._refresh()
 
 
@@ -378,17 +404,22 @@ class Attention(nn.Module):
             return self._ragged_decode(q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps)
         kv_cache.reserve(B, Hkv, past + S, D, k.dtype, k.device)
         kc, vc = kv_cache.storage()
+        if S == 1:
+            # one launch pair: the new K-hat/V row is built, written to row
+            # `past` and attended inside the decode kernel (the storage is a
+            # pool of B pages of `capacity` rows); positions as the row kernel
+            # path: position_ids (any shape broadcasting to (B, 1)), else pos_offset
+            lens, lens_next = kv_cache._step_lengths()
+            o = ops.attention_decode_paged(q4, kc, vc, kv_cache._identity_table(), lens,
+                                           max_len=past + 1, k_new=k4, v_new=v4, k_weight=kw,
+                                           lens_out=lens_next, q_weight=qw, eps=eps, cos=cos,
+                                           sin=sin, q_pos=position_ids, q_pos0=pos_offset)
+            kv_cache._step_done()
+            return self.o_proj(o.reshape(B, 1, H * D))
         ops.qk_norm_rope(k=k4, v=v4, k_out=kc, v_out=vc, k_weight=kw, eps=eps, cos=cos, sin=sin,
                          position_ids=position_ids, pos_offset=pos_offset, kv_row_offset=past)
         kv_cache.advance(S)
         T = past + S
-        if S == 1:
-            qp = None
-            if position_ids is not None:
-                qp = position_ids.reshape(B, -1)[:, 0]
-            o = ops.attention_decode(q4, kc, vc, None, max_len=T, q_weight=qw, eps=eps, cos=cos,
-                                     sin=sin, q_pos=qp, q_pos0=pos_offset)
-            return self.o_proj(o.reshape(B, 1, H * D))
         o = ops.attention_prefill(q4, kc[:, :, :T], vc[:, :, :T], q_weight=qw, eps=eps, cos=cos,
                                   sin=sin, position_ids=position_ids, pos_offset=pos_offset,
                                   causal=self.cache_prefill_causal)
@@ -400,6 +431,9 @@ class Attention(nn.Module):
         if S != 1:
             raise NotImplementedError("a ragged cache takes one token per row per step")
         Hkv = k4.shape[1]
+        if position_ids is None:
+            # the new rows sit at positions lens[b] <= seq_len
+            ops.check_position_span(0, kv_cache.seq_len + 1, self.rotary_emb.max_position_embeddings)
         kv_cache.reserve(B, Hkv, kv_cache.seq_len + 1, D, k4.dtype, k4.device)
         kc, vc = kv_cache.storage()
         kv_cache.advance(1)
@@ -407,7 +441,7 @@ class Attention(nn.Module):
         # launch appends K-hat/V at row lens[b], attends lens[b] + 1 keys and
         # writes lens + 1 into the spare lengths buffer
         lens, lens_next = kv_cache.lens, kv_cache._spare_lens()
-        qp = position_ids.reshape(B, -1)[:, 0] if position_ids is not None else None
+        qp = position_ids
         o = ops.attention_decode_paged(q4, kc, vc, kv_cache._identity_table(), lens,
                                        max_len=kv_cache.seq_len, k_new=k4, v_new=v4, k_weight=kw,
                                        lens_out=lens_next, q_weight=qw, eps=eps, cos=cos, sin=sin,
@@ -423,10 +457,12 @@ class Attention(nn.Module):
         cache._setup(B, Hkv, D, k4.dtype, k4.device)
         past = list(cache.host_lens)
         new = [n + S for n in past]
+        if position_ids is None:  # positions continue from each sequence's length
+            ops.check_position_span(0, max(new), self.rotary_emb.max_position_embeddings)
         cache._grow(new)
         if S == 1:
             lens, lens_next = cache.lens, cache._spare_lens()
-            qp = position_ids.reshape(B, -1)[:, 0] if position_ids is not None else None
+            qp = position_ids
             o = ops.attention_decode_paged(q4, cache.k_pool, cache.v_pool, cache.block_table, lens,
                                            max_len=max(new), k_new=k4, v_new=v4, k_weight=kw,
                                            lens_out=lens_next, q_weight=qw, eps=eps, cos=cos, sin=sin,

@@ -346,9 +346,11 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   // [(wave + 4i) * 1024, +1024), the lane's 16 bytes lying in tile row
   // dr0 + i * DSTEP at the same swizzled chunk for every i (the swizzle
   // repeats every 4 * 1024 bytes), so two lane constants cover the tile
-  constexpr int NPW = BW_BQ * L::RB / 1024 / 4;
+  // (a D = 32 tile is 2 KiB: waves 0 and 1 issue one instruction each)
+  constexpr int NI = BW_BQ * L::RB / 1024;  // load instructions per tile
+  constexpr int NPW = NI >= 4 ? NI / 4 : 1;
   constexpr int DSTEP = 4 * 1024 / L::RB;
-  static_assert(NPW >= 1 && (BW_BQ * L::RB) % 4096 == 0, "tile size");
+  static_assert(NI % 4 == 0 || NI < 4, "tile size");
   const int dr0 = (wave * 1024 + lane * 16) / L::RB;
   const int dlc = L::tsw(dr0, (lane * 16 % L::RB) / 16) * 8;
   // stage the (head g, query tile qt) step into buffer buf
@@ -361,6 +363,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
       const int last = p.S - qt - 1;  // rows past S clamp to the last row (masked)
 #pragma unroll
       for (int i = 0; i < NPW; ++i) {
+        if (NI < 4 && wave >= NI) break;
         const int row = min(dr0 + i * DSTEP, last);
         global_load_lds16(qsrc + (int64_t)row * p.qss + dlc, base + (wave + 4 * i) * 1024);
         global_load_lds16(dsrc + (int64_t)row * p.doss + dlc, base + TB + (wave + 4 * i) * 1024);
@@ -613,9 +616,9 @@ __global__ __launch_bounds__(256) void norm_rope_bwd_kernel(NormBwdParams p) {
     floatx8 x1 = Vec8<T>::load_f32(xr), x2 = Vec8<T>::load_f32(xr + D / 2);
     floatx8 g1 = Vec8<T>::load_f32(yr), g2 = Vec8<T>::load_f32(yr + D / 2);
     if (p.cos_tab) {
-      const int ps = clamp_pos(row_position(p.pos, p.pos_base, p.pos0, b, s, p.S), p.max_pos);
-      const floatx8 c = Vec8<float>::load_f32(p.cos_tab + (int64_t)ps * (D / 2) + sub * 8);
-      const floatx8 sn = Vec8<float>::load_f32(p.sin_tab + (int64_t)ps * (D / 2) + sub * 8);
+      const int ps = table_row(row_position(p.pos, p.pos_base, p.pos0, b, s, p.S), p.max_pos);
+      const floatx8 c = load_tab8(p.cos_tab, ps, D / 2, sub * 8);
+      const floatx8 sn = load_tab8(p.sin_tab, ps, D / 2, sub * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float d1 = g1[e], d2 = g2[e];
@@ -679,7 +682,7 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
                            const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
                            int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream) {
   nq_clear_error();
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || T <= 0)
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d S=%d T=%d)", B, Hq, Hkv, S, T);
@@ -731,9 +734,9 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NQ_DTYPE_BF16)
-    e = D == 128 ? launch_bwd<128, bf16>(p, nw, causal != 0, st) : launch_bwd<64, bf16>(p, nw, causal != 0, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_bwd<decltype(dc)::value, bf16>(p, nw, causal != 0, st); });
   else
-    e = D == 128 ? launch_bwd<128, float>(p, nw, causal != 0, st) : launch_bwd<64, float>(p, nw, causal != 0, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_bwd<decltype(dc)::value, float>(p, nw, causal != 0, st); });
   return nq_check_launch(e);
 }
 
@@ -743,7 +746,7 @@ extern "C" int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, cons
                                    float eps, const float* cos_tab, const float* sin_tab, int max_pos,
                                    const int32_t* pos, const int32_t* pos_base, int pos0, void* stream) {
   nq_clear_error();
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || S <= 0 || H <= 0) return nq_fail(NQ_ERR_INVALID, "sizes must be positive");
   if (!x || !dy || !dx || !x_strides || !dy_strides || !dx_strides)
@@ -771,12 +774,11 @@ extern "C" int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, cons
   const int64_t blocks = (rows + rpb - 1) / rpb;
   const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == NQ_DTYPE_BF16) {
-    if (D == 128) hipLaunchKernelGGL((norm_rope_bwd_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((norm_rope_bwd_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
-  } else {
-    if (D == 128) hipLaunchKernelGGL((norm_rope_bwd_kernel<float, 128>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((norm_rope_bwd_kernel<float, 64>), grid, dim3(256), 0, st, p);
-  }
+  with_head_dim(D, [&](auto dc) {
+    constexpr int DD = decltype(dc)::value;
+    if (dtype == NQ_DTYPE_BF16) hipLaunchKernelGGL((norm_rope_bwd_kernel<bf16, DD>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((norm_rope_bwd_kernel<float, DD>), grid, dim3(256), 0, st, p);
+    return 0;
+  });
   return nq_check_launch(hipGetLastError());
 }

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace nq {
 
 typedef __bf16 bf16;
@@ -173,6 +175,12 @@ __device__ __forceinline__ void store8<float>(float* p, floatx8 v) {
 }
 
 template <typename T>
+__device__ __forceinline__ void store2(T* p, float a, float b) {
+  p[0] = (T)a;
+  p[1] = (T)b;
+}
+
+template <typename T>
 __device__ __forceinline__ void store4(T* p, floatx4 v);
 template <>
 __device__ __forceinline__ void store4<bf16>(bf16* p, floatx4 v) {
@@ -200,16 +208,43 @@ __device__ __forceinline__ float xor32_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Sum over groups of LPR = 4 or 8 consecutive lanes with DPP (all VALU).
+// Sum over groups of LPR = 2, 4 or 8 consecutive lanes with DPP (all VALU).
 template <int LPR>
 __device__ __forceinline__ float row_sum(float v) {
-  static_assert(LPR == 4 || LPR == 8, "groups of 4 or 8 lanes");
+  static_assert(LPR == 2 || LPR == 4 || LPR == 8, "groups of 2, 4 or 8 lanes");
   if (LPR == 8) {  // lane i <- lane 7-i within each group of 8
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
   }
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad xor 1
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad xor 2
+  if (LPR >= 4)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad xor 2
   return v;
+}
+
+// Head dims every kernel is built for, and the host-side switch that calls
+// f(std::integral_constant<int, D>) for the one asked for.
+constexpr bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128; }
+template <typename F>
+inline auto with_head_dim(int D, F&& f) {
+  if (D == 32) return f(std::integral_constant<int, 32>{});
+  if (D == 64) return f(std::integral_constant<int, 64>{});
+  return f(std::integral_constant<int, 128>{});
+}
+
+// RoPE table row of position p: p itself when 0 <= p < max_pos, else -1.
+// Rows at an out-of-range position rotate with NaN cos/sin, so every value
+// they reach comes out NaN (the reference's table lookup, model/rope.py:128,
+// fails on such positions; callers that know positions on the host check them
+// there).
+__device__ __forceinline__ int table_row(int p, int max_pos) { return (p >= 0 && p < max_pos) ? p : -1; }
+// 8 consecutive table values of row `row` (from table_row) at column `col`
+// of a table with `width` columns; NaN for row -1.
+__device__ __forceinline__ floatx8 load_tab8(const float* tab, int row, int width, int col) {
+  if (row < 0) {
+    const float n = __builtin_nanf("");
+    return floatx8{n, n, n, n, n, n, n, n};
+  }
+  return Vec8<float>::load_f32(tab + (int64_t)row * width + col);
 }
 
 // One head_dim row held by D/16 lanes: lane `sub` owns elements [8sub, 8sub+8)
@@ -251,8 +286,8 @@ __device__ __forceinline__ void norm_rope_row(floatx8& x1, floatx8& x2, const fl
                                               int sub) {
   if (w1) norm_row<D>(x1, x2, *w1, *w2, eps);
   if (cos_tab) {
-    const floatx8 c = Vec8<float>::load_f32(cos_tab + (int64_t)pos * (D / 2) + sub * 8);
-    const floatx8 sn = Vec8<float>::load_f32(sin_tab + (int64_t)pos * (D / 2) + sub * 8);
+    const floatx8 c = load_tab8(cos_tab, pos, D / 2, sub * 8);
+    const floatx8 sn = load_tab8(sin_tab, pos, D / 2, sub * 8);
     rope_row(x1, x2, c, sn);
   }
 }
@@ -264,8 +299,5 @@ __device__ __forceinline__ int row_position(const int32_t* pos, const int32_t* p
   return (pos_base ? pos_base[b] : pos0) + s;
 }
 
-__device__ __forceinline__ int clamp_pos(int p, int max_pos) {
-  return p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
-}
 
 }  // namespace nq

@@ -140,9 +140,14 @@ template <> struct Piece<float> {
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // ---------------------------------------------------------------- schedule
-// Keys attended by batch row b (the appended key included).
+// Keys attended by batch row b (the appended key included), or -1 for a row
+// whose length lies outside [0, max_len - append]: such a row attends
+// nothing, appends nothing and its output is NaN (a cache row past max_len is
+// not the caller's to give).
 __device__ __forceinline__ int batch_len(const DecodeParams& p, int b) {
-  return p.lens ? min(p.lens[b] + p.append, p.max_len) : p.max_len;
+  if (!p.lens) return p.max_len;
+  const int l = p.lens[b];
+  return (l < 0 || l > p.max_len - p.append) ? -1 : l + p.append;
 }
 __device__ __forceinline__ int batch_steps(const DecodeParams& p, int b) {
   const int len = batch_len(p, b);
@@ -323,7 +328,11 @@ decode_stream_kernel(DecodeParams p) {
     const bool hvalid = gh < p.G;
     const int head = kvh * p.G + (hvalid ? gh : 0);
     const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh;
-    floatx8 xf[NDQ], wq[NDQ], cs[NDQ / 2], sn[NDQ / 2];
+    // cos/sin of this lane's elements: for D >= 64 the rotate-half partners sit
+    // in the same lane (d blocks dq and dq + NDQ/2); for D = 32 (one d block)
+    // element d of lanes 0..31 pairs with d + 16 of lanes 32..63
+    constexpr int NCS = NDQ >= 2 ? NDQ / 2 : 1;
+    floatx8 xf[NDQ], wq[NDQ], cs[NCS], sn[NCS];
 #pragma unroll
     for (int dq = 0; dq < NDQ; ++dq) xf[dq] = Vec8<T>::load_f32(qrow + dq * 32 + grp * 8);
     if (p.qw) {
@@ -331,18 +340,17 @@ decode_stream_kernel(DecodeParams p) {
       for (int dq = 0; dq < NDQ; ++dq) wq[dq] = Vec8<float>::load_f32(p.qw + dq * 32 + grp * 8);
     }
     const int pos =
-        p.cos_tab ? clamp_pos(p.q_pos ? uniform(p.q_pos[b]) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos) : 0;
+        p.cos_tab ? table_row(p.q_pos ? uniform(p.q_pos[b]) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos) : 0;
     if (p.cos_tab) {
-      const float* ct = p.cos_tab + (int64_t)pos * (D / 2);
-      const float* st = p.sin_tab + (int64_t)pos * (D / 2);
 #pragma unroll
-      for (int dq = 0; dq < NDQ / 2; ++dq) {
-        cs[dq] = Vec8<float>::load_f32(ct + dq * 32 + grp * 8);
-        sn[dq] = Vec8<float>::load_f32(st + dq * 32 + grp * 8);
+      for (int dq = 0; dq < NCS; ++dq) {
+        const int col = NDQ >= 2 ? dq * 32 + grp * 8 : (grp & 1) * 8;
+        cs[dq] = load_tab8(p.cos_tab, pos, D / 2, col);
+        sn[dq] = load_tab8(p.sin_tab, pos, D / 2, col);
       }
       if (tail) {  // the appended key is rotated at the query's position
-        kc1 = Vec8<float>::load_f32(ct + sub * 8);
-        ks1 = Vec8<float>::load_f32(st + sub * 8);
+        kc1 = load_tab8(p.cos_tab, pos, D / 2, sub * 8);
+        ks1 = load_tab8(p.sin_tab, pos, D / 2, sub * 8);
       }
     }
 
@@ -414,13 +422,23 @@ decode_stream_kernel(DecodeParams p) {
           for (int e = 0; e < 8; ++e) xf[dq][e] = xf[dq][e] * r * wq[dq][e];
       }
       if (p.cos_tab) {
+        if constexpr (NDQ >= 2) {
 #pragma unroll
-        for (int dq = 0; dq < NDQ / 2; ++dq) {
-          floatx8 x1 = xf[dq], x2 = xf[dq + NDQ / 2];
+          for (int dq = 0; dq < NDQ / 2; ++dq) {
+            floatx8 x1 = xf[dq], x2 = xf[dq + NDQ / 2];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              xf[dq][e] = x1[e] * cs[dq][e] - x2[e] * sn[dq][e];
+              xf[dq + NDQ / 2][e] = x2[e] * cs[dq][e] + x1[e] * sn[dq][e];
+            }
+          }
+        } else {
+          // first half (lanes < 32): x1 c - x2 s; second half: x2 c + x1 s
+          const float sg = lane < 32 ? -1.f : 1.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            xf[dq][e] = x1[e] * cs[dq][e] - x2[e] * sn[dq][e];
-            xf[dq + NDQ / 2][e] = x2[e] * cs[dq][e] + x1[e] * sn[dq][e];
+            const float partner = __shfl_xor(xf[0][e], 32, 64);
+            xf[0][e] = xf[0][e] * cs[0][e] + sg * (partner * sn[0][e]);
           }
         }
       }
@@ -542,19 +560,21 @@ decode_stream_kernel(DecodeParams p) {
 // Thread t owns head t / 16 of the group and DPT consecutive dims.
 template <int D, typename T>
 __global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p) {
-  constexpr int DPT = D / 16;  // dims per thread (8 or 4)
+  constexpr int DPT = D / 16;  // dims per thread (8, 4 or 2)
   const int64_t r = blockIdx.x;
   const int b = (int)(r / p.rows_per_batch), j = (int)(r % p.rows_per_batch);
   const int kvh = j / p.NG, hg = j % p.NG;
   const int hq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * DPT;
   const int gh = hg * 16 + hq;
-  if (p.lens_out && j == 0 && threadIdx.x == 0) p.lens_out[b] = p.lens[b] + 1;
-  const int nb = uniform(batch_steps(p, b));
+  const int len = uniform(batch_len(p, b));
+  if (p.lens_out && j == 0 && threadIdx.x == 0) p.lens_out[b] = len < 0 ? p.lens[b] : p.lens[b] + 1;
   T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (int64_t)(kvh * p.G + (gh < p.G ? gh : 0)) * p.osh + d0;
-  if (nb == 0) {
+  if (len <= 0) {  // no keys: zeros; a length out of range: NaN
     if (gh < p.G) {
-      if constexpr (DPT == 8) store8<T>(orow, floatx8{});
-      else store4<T>(orow, floatx4{});
+      const float f = len < 0 ? __builtin_nanf("") : 0.f;
+      if constexpr (DPT == 8) store8<T>(orow, floatx8{f, f, f, f, f, f, f, f});
+      else if constexpr (DPT == 4) store4<T>(orow, floatx4{f, f, f, f});
+      else store2<T>(orow, f, f);
     }
     return;
   }
@@ -574,19 +594,27 @@ __global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p
     const floatx2 m_l = *reinterpret_cast<const floatx2*>(ml + i * 32);
     const float sc = fast_exp2(m_l[0] - M);
     wsum += m_l[1] * sc;
+    if constexpr (DPT == 2) {
+      const floatx2 o2 = *reinterpret_cast<const floatx2*>(po + (int64_t)i * 16 * D);
+      acc[0] += o2[0] * sc;
+      acc[1] += o2[1] * sc;
+    } else {
 #pragma unroll
-    for (int e = 0; e < DPT; e += 4) {
-      const floatx4 o4 = *reinterpret_cast<const floatx4*>(po + (int64_t)i * 16 * D + e);
+      for (int e = 0; e < DPT; e += 4) {
+        const floatx4 o4 = *reinterpret_cast<const floatx4*>(po + (int64_t)i * 16 * D + e);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc[e + k] += o4[k] * sc;
+        for (int k = 0; k < 4; ++k) acc[e + k] += o4[k] * sc;
+      }
     }
   }
   const float inv = 1.0f / wsum;
   if constexpr (DPT == 8) {
     store8<T>(orow, floatx8{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv,
                             acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv});
-  } else {
+  } else if constexpr (DPT == 4) {
     store4<T>(orow, floatx4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv});
+  } else {
+    store2<T>(orow, acc[0] * inv, acc[1] * inv);
   }
 }
 
@@ -646,7 +674,7 @@ static int decode_setup(DecodeParams& p, const void* q, const int64_t* q_strides
                         int64_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_len, int chunk,
                         int dtype, const float* q_weight, float eps, const float* cos_tab,
                         const float* sin_tab, int max_pos, const int32_t* q_pos, int q_pos0, float sm_scale) {
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0)
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d max_len=%d)", B, Hq, Hkv, max_len);
@@ -696,9 +724,9 @@ static int decode_launch(const DecodeParams& p, int D, int dtype, void* stream) 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NQ_DTYPE_BF16)
-    e = (D == 128) ? launch_decode<128, bf16, PAGED, APPEND>(p, st) : launch_decode<64, bf16, PAGED, APPEND>(p, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_decode<decltype(dc)::value, bf16, PAGED, APPEND>(p, st); });
   else
-    e = (D == 128) ? launch_decode<128, float, PAGED, APPEND>(p, st) : launch_decode<64, float, PAGED, APPEND>(p, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_decode<decltype(dc)::value, float, PAGED, APPEND>(p, st); });
   return nq_check_launch(e);
 }
 

@@ -80,7 +80,7 @@ extern "C" int nq_attn_merge(void* o, const int64_t* o_strides, float* lse, cons
                              const int64_t* part_strides, const float* lse_part, int B, int H, int S,
                              int D, int dtype, void* stream) {
   nq_clear_error();
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || H <= 0 || S <= 0) return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d H=%d S=%d)", B, H, S);
   if (!o || !lse || !o_part || !lse_part || !o_strides || !part_strides)
@@ -100,8 +100,8 @@ extern "C" int nq_attn_merge(void* o, const int64_t* o_strides, float* lse, cons
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NQ_DTYPE_BF16)
-    e = D == 128 ? launch_merge<bf16, 128>(p, st) : launch_merge<bf16, 64>(p, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_merge<bf16, decltype(dc)::value>(p, st); });
   else
-    e = D == 128 ? launch_merge<float, 128>(p, st) : launch_merge<float, 64>(p, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_merge<float, decltype(dc)::value>(p, st); });
   return nq_check_launch(e);
 }

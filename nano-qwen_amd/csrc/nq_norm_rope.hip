@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
   constexpr int LPR = D / 16;         // lanes per row
   constexpr int RPW = 64 / LPR;       // rows per wave
   constexpr int RPB = RPW * 4;        // rows per 256-thread block and unroll step
-  static_assert(LPR == 4 || LPR == 8, "D must be 64 or 128");
+  static_assert(LPR == 2 || LPR == 4 || LPR == 8, "D must be 32, 64 or 128");
   const RowJob& jb = p.job[blockIdx.y];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
   }
 #pragma unroll
   for (int u = 0; u < ROW_UNROLL; ++u) {
-    const int pos = jb.rope ? clamp_pos(row_position(p.pos, p.pos_base, p.pos0, bb[u], ss_[u], p.S), p.max_pos) : 0;
+    const int pos = jb.rope ? table_row(row_position(p.pos, p.pos_base, p.pos0, bb[u], ss_[u], p.S), p.max_pos) : 0;
     norm_rope_row<D>(x1[u], x2[u], jb.norm ? &w1 : nullptr, &w2, p.eps, jb.rope ? p.cos_tab : nullptr,
                      p.sin_tab, pos, sub);
     if (act[u]) {
@@ -141,7 +141,7 @@ static int qk_norm_rope_impl(const void* q, const int64_t* q_strides, void* q_ou
                              const int32_t* kv_row_base, int kv_row0, const int32_t* block_table,
                              int64_t bt_stride, int page_size, void* stream) {
   nq_clear_error();
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (B <= 0 || S <= 0) return nq_fail(NQ_ERR_INVALID, "B and S must be positive (B=%d S=%d)", B, S);
   if (!nq_dtype_ok(dtype_in) || !nq_dtype_ok(dtype_out))
     return nq_fail(NQ_ERR_UNSUPPORTED, "dtype codes must be NQ_DTYPE_BF16 or NQ_DTYPE_F32");
@@ -182,8 +182,8 @@ static int qk_norm_rope_impl(const void* q, const int64_t* q_strides, void* q_ou
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   const bool bi = dtype_in == NQ_DTYPE_BF16, bo = dtype_out == NQ_DTYPE_BF16;
-#define NQ_ROWS(TI, TO)                                                               \
-  e = (D == 128) ? launch_rows<TI, TO, 128>(p, max_h, st) : launch_rows<TI, TO, 64>(p, max_h, st)
+#define NQ_ROWS(TI, TO) \
+  e = with_head_dim(D, [&](auto dc) { return launch_rows<TI, TO, decltype(dc)::value>(p, max_h, st); })
   if (bi && bo) NQ_ROWS(bf16, bf16);
   else if (bi && !bo) NQ_ROWS(bf16, float);
   else if (!bi && bo) NQ_ROWS(float, bf16);
@@ -230,4 +230,88 @@ extern "C" int nq_kv_append_paged(const void* k, const int64_t* k_strides, const
                            v_strides, v_pool, v_pool_strides, B, S, 0, Hkv, D, dtype_in, dtype_out,
                            nullptr, k_weight, eps, cos_tab, sin_tab, max_pos, pos, pos_base, pos0,
                            row_base, row0, block_table, bt_stride, page_size, stream);
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// RMSNorm.forward of model/norm.py:17-22 over rows of any width (a multiple
+// of 8): y = round_x(x * rsqrt(mean(x^2) + eps)) * w, where round_x is the
+// cast back to the input dtype (`.type_as(x)`) and the product is formed in
+// fp32 and stored in the promoted dtype of x and w -- the reference's cast
+// order and dtype promotion.  One wave per row; lane l holds the 8-element
+// chunks l, l + 64, ...; the sum of squares is a wave reduction.
+namespace nq {
+
+struct RmsParams {
+  const void* x;
+  int64_t xs;  // row stride (elements)
+  const void* w;
+  void* y;
+  int64_t ys;
+  int64_t rows;
+  int width;
+  float eps;
+};
+
+template <typename T>
+__device__ __forceinline__ float round_to(float v) {
+  return (float)(T)v;
+}
+
+template <typename TI, typename TW, typename TO>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(RmsParams p) {
+  const int lane = threadIdx.x & 63;
+  const int nch = p.width / 8;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < p.rows; row += (int64_t)gridDim.x * 4) {
+    const TI* xr = reinterpret_cast<const TI*>(p.x) + row * p.xs;
+    float ss = 0.f;
+    for (int c = lane; c < nch; c += 64) {
+      const floatx8 v = Vec8<TI>::load_f32(xr + c * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float r = rsqrtf(ss / (float)p.width + p.eps);
+    TO* yr = reinterpret_cast<TO*>(p.y) + row * p.ys;
+    for (int c = lane; c < nch; c += 64) {
+      const floatx8 v = Vec8<TI>::load_f32(xr + c * 8);
+      const floatx8 wv = Vec8<TW>::load_f32(reinterpret_cast<const TW*>(p.w) + c * 8);
+      floatx8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = round_to<TI>(v[e] * r) * wv[e];
+      store8<TO>(yr + c * 8, o);
+    }
+  }
+}
+
+}  // namespace nq
+
+extern "C" int nq_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, void* y,
+                          int64_t y_row_stride, int64_t rows, int width, int dtype_x, int dtype_w,
+                          int dtype_y, float eps, void* stream) {
+  nq_clear_error();
+  if (!nq_dtype_ok(dtype_x) || !nq_dtype_ok(dtype_w) || !nq_dtype_ok(dtype_y))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "dtype codes must be NQ_DTYPE_BF16 or NQ_DTYPE_F32");
+  // the promoted dtype: fp32 unless both x and w are bf16
+  const int promoted = (dtype_x == NQ_DTYPE_BF16 && dtype_w == NQ_DTYPE_BF16) ? NQ_DTYPE_BF16 : NQ_DTYPE_F32;
+  if (dtype_y != promoted)
+    return nq_fail(NQ_ERR_INVALID, "y must have the promoted dtype of x and weight (code %d)", promoted);
+  if (rows < 0 || width <= 0 || width % 8)
+    return nq_fail(NQ_ERR_UNSUPPORTED, "width must be a positive multiple of 8, got %d", width);
+  if (rows == 0) return NQ_OK;
+  if (!x || !weight || !y) return nq_fail(NQ_ERR_INVALID, "x, weight and y are required");
+  if (!nq_aligned16(x) || !nq_aligned16(weight) || !nq_aligned16(y))
+    return nq_fail(NQ_ERR_INVALID, "base pointers must be 16-byte aligned");
+  if ((x_row_stride * nq_dtype_size(dtype_x)) % 16 || (y_row_stride * nq_dtype_size(dtype_y)) % 16)
+    return nq_fail(NQ_ERR_INVALID, "row strides must be multiples of 16 bytes");
+  RmsParams p{x, x_row_stride, weight, y, y_row_stride, rows, width, eps};
+  const int64_t blocks = (rows + 3) / 4;
+  const dim3 grid((unsigned)(blocks < 2048 ? blocks : 2048));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool bx = dtype_x == NQ_DTYPE_BF16, bw = dtype_w == NQ_DTYPE_BF16;
+  if (bx && bw) hipLaunchKernelGGL((rmsnorm_rows_kernel<bf16, bf16, bf16>), grid, dim3(256), 0, st, p);
+  else if (bx) hipLaunchKernelGGL((rmsnorm_rows_kernel<bf16, float, float>), grid, dim3(256), 0, st, p);
+  else if (bw) hipLaunchKernelGGL((rmsnorm_rows_kernel<float, bf16, float>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((rmsnorm_rows_kernel<float, float, float>), grid, dim3(256), 0, st, p);
+  return nq_check_launch(hipGetLastError());
 }

@@ -212,13 +212,11 @@ prefill_kernel(PrefillParams p) {
         }
       }
       if (p.cos_tab) {
-        const int pos = clamp_pos(row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S), p.max_pos);
-        const float* ct = p.cos_tab + (int64_t)pos * (D / 2);
-        const float* st = p.sin_tab + (int64_t)pos * (D / 2);
+        const int pos = table_row(row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S), p.max_pos);
 #pragma unroll
         for (int db = 0; db < NDB / 2; ++db) {
-          floatx8 c = Vec8<float>::load_f32(ct + db * 16 + hh * 8);
-          floatx8 s = Vec8<float>::load_f32(st + db * 16 + hh * 8);
+          floatx8 c = load_tab8(p.cos_tab, pos, D / 2, db * 16 + hh * 8);
+          floatx8 s = load_tab8(p.sin_tab, pos, D / 2, db * 16 + hh * 8);
           floatx8 x1 = xf[db], x2 = xf[db + NDB / 2];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -477,7 +475,12 @@ static hipError_t launch_prefill_nw(const PrefillParams& p, bool causal, bool fu
 
 template <int D, typename T>
 static hipError_t launch_prefill(const PrefillParams& p, int nw, bool causal, bool fuse, hipStream_t st) {
-  return nw == 8 ? launch_prefill_nw<D, T, 8>(p, causal, fuse, st) : launch_prefill_nw<D, T, 4>(p, causal, fuse, st);
+  if constexpr (D == 32) {
+    if (nw != 4) return hipErrorInvalidValue;  // one 1 KiB tile load per wave needs 4 waves
+    return launch_prefill_nw<D, T, 4>(p, causal, fuse, st);
+  } else {
+    return nw == 8 ? launch_prefill_nw<D, T, 8>(p, causal, fuse, st) : launch_prefill_nw<D, T, 4>(p, causal, fuse, st);
+  }
 }
 
 }  // namespace nq
@@ -493,13 +496,15 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
                                    const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
                                    int causal, float sm_scale, void* stream) {
   nq_clear_error();
-  if (D != 64 && D != 128) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %d", D);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || T <= 0)
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d S=%d T=%d)", B, Hq, Hkv, S, T);
   if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
   const int G = Hq / Hkv;
   if (PF_MAX_ROWS % G) return nq_fail(NQ_ERR_UNSUPPORTED, "GQA group size %d must divide %d", G, PF_MAX_ROWS);
+  if (D == 32 && 128 % G)
+    return nq_fail(NQ_ERR_UNSUPPORTED, "at head_dim 32 the GQA group size %d must divide 128", G);
   if (causal && S > T) return nq_fail(NQ_ERR_INVALID, "causal attention needs S <= T (S=%d T=%d)", S, T);
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides)
     return nq_fail(NQ_ERR_INVALID, "q, k, v, o and their strides are required");
@@ -529,7 +534,9 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
   // 256 rows per workgroup when that still gives enough workgroups, else 128
   const int64_t wide_wgs = (int64_t)B * Hkv * ((S + PF_MAX_ROWS / G - 1) / (PF_MAX_ROWS / G));
-  const int nw = (128 % G == 0 && wide_wgs < PF_WIDE_MIN_WGS) ? 4 : 8;
+  // (a D = 32 tile is 4 KiB: one 1 KiB load per wave of a 4-wave workgroup,
+  // too few for eight waves)
+  const int nw = (128 % G == 0 && (wide_wgs < PF_WIDE_MIN_WGS || D == 32)) ? 4 : 8;
   p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
@@ -538,8 +545,8 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NQ_DTYPE_BF16)
-    e = (D == 128) ? launch_prefill<128, bf16>(p, nw, causal, fuse, st) : launch_prefill<64, bf16>(p, nw, causal, fuse, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_prefill<decltype(dc)::value, bf16>(p, nw, causal, fuse, st); });
   else
-    e = (D == 128) ? launch_prefill<128, float>(p, nw, causal, fuse, st) : launch_prefill<64, float>(p, nw, causal, fuse, st);
+    e = with_head_dim(D, [&](auto dc) { return launch_prefill<decltype(dc)::value, float>(p, nw, causal, fuse, st); });
   return nq_check_launch(e);
 }

@@ -1,8 +1,11 @@
 """RMSNorm module with the reference's parameter layout (model/norm.py:11-22).
 
-Used as QK-Norm by ``Attention``; there the normalisation is fused into the
-HIP kernels, which read ``weight`` as fp32.  The module's own ``forward`` on a
-device tensor of shape (..., head_dim) runs the gfx950 row kernel.
+``Attention`` fuses QK-Norm into its HIP kernels, which read ``weight`` as
+fp32.  The module's own ``forward`` runs ``nq_rmsnorm``: rows of any width (a
+multiple of 8), the reference's cast order (the normalised value is cast back
+to ``x.dtype`` before the weight multiply) and its dtype promotion (a bf16
+input with an fp32 weight gives fp32, as ``output.type_as(x) * weight`` does).
+Under autograd the backward is ``nq_qk_norm_rope_bwd`` (widths 32, 64, 128).
 """
 
 from __future__ import annotations
@@ -13,6 +16,42 @@ import torch.nn as nn
 from . import _lib, ops
 
 
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """model/norm.py:20-22 on the device: (x, weight) -> y in their promoted dtype."""
+    ops._require_device(x, weight)
+    W = x.shape[-1]
+    if W % 8:
+        raise ValueError(f"nq_rmsnorm takes widths that are multiples of 8, got {W}")
+    out_dtype = torch.promote_types(x.dtype, weight.dtype)
+    rows = x.reshape(-1, W)
+    if rows.stride(-1) != 1 or not ops._aligned(rows):
+        rows = rows.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    y = torch.empty(rows.shape, dtype=out_dtype, device=x.device)
+    rc = _lib.load().nq_rmsnorm(ops._ptr(rows), rows.stride(0), ops._ptr(w), ops._ptr(y), y.stride(0),
+                                rows.shape[0], W, ops._code(rows), ops._code(w), ops._code(y), float(eps),
+                                ops._stream(x))
+    _lib.check(rc, "nq_rmsnorm")
+    return y.view(x.shape)
+
+
+class _RMSNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, eps: float):
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        return rms_norm(x, weight, eps)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        W = x.shape[-1]
+        x4 = x.reshape(1, 1, -1, W)
+        dy4 = dy.to(x.dtype).reshape(1, 1, -1, W)
+        dx, dw = ops.qk_norm_rope_backward(x4, dy4, weight=weight, eps=ctx.eps)
+        return dx.reshape(x.shape), dw.to(weight.dtype), None
+
+
 class RMSNorm(nn.Module):
     def __init__(self, hidden_size: int, eps: float = 1e-6):
         super().__init__()
@@ -20,24 +59,8 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        """RMSNorm over the last dim, fp32 arithmetic, output in x.dtype.
-
-        Rows of 64 or 128 elements run on the row kernel; other widths are not
-        part of the attention path and raise.
-        """
-        D = x.shape[-1]
-        if D not in (64, 128):
-            raise ValueError(f"RMSNorm kernel supports head_dim 64 or 128, got {D}")
-        ops._require_device(x)
-        rows = ops._rows_in(x.reshape(1, 1, -1, D))
-        out = torch.empty(rows.shape, dtype=x.dtype, device=x.device)
-        lib = _lib.load()
-        st = _lib.strides3
-        rc = lib.nq_qk_norm_rope(
-            ops._ptr(rows), st(rows.stride()[:3]), ops._ptr(out),
-            st(out.stride()[:3]), None, None, None, None, None, None, None, None,
-            1, rows.shape[2], 1, 1, D, ops._code(x), ops._code(out),
-            ops._ptr(ops._f32(self.weight, x.device)), None, float(self.eps),
-            None, None, 0, None, None, 0, None, 0, ops._stream(x))
-        _lib.check(rc, "RMSNorm")
-        return out.view(x.shape)
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
+            if x.shape[-1] not in (32, 64, 128):
+                raise NotImplementedError("RMSNorm's backward kernel covers widths 32, 64 and 128")
+            return _RMSNormFn.apply(x, self.weight, self.eps)
+        return rms_norm(x, self.weight, self.eps)

@@ -106,6 +106,49 @@ def _tables(cos, sin, device):
     return c, s, c.shape[0]
 
 
+def _range_error(lo: int, hi: int, max_pos: int) -> IndexError:
+    return IndexError(f"positions {lo}..{hi} lie outside the RoPE table of {max_pos} positions "
+                      "(max_position_embeddings)")
+
+
+def check_position_span(first: int, count: int, max_pos: int) -> None:
+    """Raise IndexError unless positions first .. first+count-1 index the table.
+
+    The reference's table lookup (model/rope.py:123-129) fails on such
+    positions; the kernels cannot raise, and rotate a row at an out-of-range
+    position with NaN instead.
+    """
+    if count > 0 and max_pos > 0 and (first < 0 or first + count > max_pos):
+        raise _range_error(first, first + count - 1, max_pos)
+
+
+def _check_host_positions(pos: Optional[torch.Tensor], max_pos: int) -> None:
+    """Range check of positions held on the host (a device tensor is not read back)."""
+    if pos is None or max_pos <= 0 or pos.is_cuda or pos.numel() == 0:
+        return
+    lo, hi = int(pos.min()), int(pos.max())
+    if lo < 0 or hi >= max_pos:
+        raise _range_error(lo, hi, max_pos)
+
+
+def _positions(position_ids: Optional[torch.Tensor], pos_offset: int, pos_base: Optional[torch.Tensor],
+               B: int, S: int, max_pos: int, dev) -> Optional[torch.Tensor]:
+    """int32 (B, S) device positions, or None when they follow pos_base / pos_offset.
+
+    Positions the host knows are range-checked here: explicit host
+    ``position_ids``, and ``pos_offset .. pos_offset + S - 1``.
+    """
+    if position_ids is not None:
+        _check_host_positions(position_ids, max_pos)
+        pos = _i32(position_ids, dev)
+        if tuple(pos.shape) != (B, S):
+            pos = pos.expand(B, S).contiguous()
+        return pos
+    if pos_base is None:
+        check_position_span(int(pos_offset), S, max_pos)
+    return None
+
+
 class KernelCall:
     """A validated, fully bound call into libnqattn.so.
 
@@ -186,9 +229,7 @@ def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = N
         if src is not None and kv_row_base is None and kv_row_offset + S > dst.shape[2]:
             raise ValueError(f"{name}_out has {dst.shape[2]} rows; rows up to {kv_row_offset + S} needed")
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
-    pos = _i32(position_ids, dev)
-    if pos is not None and tuple(pos.shape) != (B, S):
-        pos = pos.expand(B, S).contiguous()
+    pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
     pb = _i32(pos_base, dev)
     rb = _i32(kv_row_base, dev)
     qw, kw = _f32(q_weight, dev), _f32(k_weight, dev)
@@ -254,9 +295,7 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     lse = torch.empty(B, Hq, S, dtype=torch.float32, device=q.device) if return_lse else None
     dev = q.device
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
-    pos = _i32(position_ids, dev)
-    if pos is not None and tuple(pos.shape) != (B, S):
-        pos = pos.expand(B, S).contiguous()
+    pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
     pb = _i32(pos_base, dev)
     qw = _f32(q_weight, dev)
     st = _lib.strides3
@@ -274,6 +313,22 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 # ---------------------------------------------------------------------------
 # Decode
 # ---------------------------------------------------------------------------
+
+def _decode_q_pos(q_pos: Optional[torch.Tensor], q_pos0: int, B: int, max_pos: int, dev):
+    """int32 (B,) query positions from q_pos (any shape broadcastable to (B, 1),
+    e.g. position_ids of a one-token step), with the host-known ones range-checked."""
+    if q_pos is None:
+        if q_pos0 >= 0:
+            check_position_span(int(q_pos0), 1, max_pos)
+        return None
+    _check_host_positions(q_pos, max_pos)
+    qp = q_pos.reshape(-1, q_pos.shape[-1])[:, -1] if q_pos.dim() > 1 else q_pos.reshape(-1)
+    if qp.numel() == 1 and B > 1:
+        qp = qp.expand(B)
+    if qp.numel() != B:
+        raise ValueError(f"q_pos must give one position per batch row ({B}), got shape {tuple(q_pos.shape)}")
+    return _i32(qp, dev)
+
 
 def decode_workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_len: int, chunk: int = 0) -> int:
     """Workspace size attention_decode needs for these sizes."""
@@ -320,7 +375,7 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
     lens_t = _i32(lens, dev)
-    qp = _i32(q_pos, dev)
+    qp = _decode_q_pos(q_pos, q_pos0, B, max_pos, dev)
     qw = _f32(q_weight, dev)
     q_str = (ctypes.c_int64 * 2)(q.stride(0), q.stride(1))
     o_str = (ctypes.c_int64 * 2)(out.stride(0), out.stride(1))
@@ -390,9 +445,7 @@ def kv_append_paged(k: Optional[torch.Tensor], v: Optional[torch.Tensor], k_pool
     k = _rows_in(k) if k is not None else None
     v = _rows_in(v) if v is not None else None
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
-    pos = _i32(position_ids, dev)
-    if pos is not None and tuple(pos.shape) != (B, S):
-        pos = pos.expand(B, S).contiguous()
+    pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
     pb = _i32(pos_base, dev)
     rb = _i32(row_base, dev)
     kw = _f32(k_weight, dev)
@@ -479,7 +532,7 @@ def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
-    qp = _i32(q_pos, dev)
+    qp = _decode_q_pos(q_pos, q_pos0, B, max_pos, dev)
     qw, kw = _f32(q_weight, dev), _f32(k_weight, dev)
     q_str = (ctypes.c_int64 * 2)(q.stride(0), q.stride(1))
     o_str = (ctypes.c_int64 * 2)(out.stride(0), out.stride(1))
@@ -601,9 +654,7 @@ def qk_norm_rope_backward(x: torch.Tensor, dy: torch.Tensor, *, weight: Optional
     w = _f32(weight, dev)
     dw = torch.zeros(D, dtype=torch.float32, device=dev) if w is not None else None
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
-    pos = _i32(position_ids, dev)
-    if pos is not None and tuple(pos.shape) != (B, S):
-        pos = pos.expand(B, S).contiguous()
+    pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
     pb = _i32(pos_base, dev)
     st = _lib.strides3
     rc = _lib.load().nq_qk_norm_rope_bwd(

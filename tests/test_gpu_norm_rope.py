@@ -97,5 +97,10 @@ def test_rmsnorm_module_matches_oracle():
     with torch.no_grad():
         norm.weight.copy_(1 + 0.1 * randn(128, seed=11))
     y = norm.to(DEV)(x.to(DEV))
-    assert y.dtype == torch.bfloat16
-    assert_bf16_close(y, rms_norm(x.float(), norm.weight.detach().cpu(), 1e-6), "rmsnorm")
+    # model/norm.py:21-22: `.type_as(x) * weight` promotes a bf16 input with an
+    # fp32 weight to fp32 (the golden tests/golden/rmsnorm.npz records it)
+    ref = rms_norm(x, norm.weight.detach().cpu(), 1e-6)
+    assert y.dtype == ref.dtype == torch.float32
+    assert_bf16_close(y, ref, "rmsnorm")
+    y.float().sum().backward()  # autograd through the backward kernel
+    assert norm.weight.grad is not None and torch.isfinite(norm.weight.grad).all()
