@@ -209,6 +209,32 @@ int nq_attn_decode_paged_fwd(const void* q, const int64_t* q_strides, const void
                              const int32_t* q_pos, int q_pos0, float sm_scale, void* stream);
 
 /*
+ * nq_attn_decode_paged_fwd without a workspace argument, allocating nothing.
+ * It has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a static device array
+ * of NQ_DECODE_SCRATCH_BYTES that each GPU the library runs on holds until
+ * the process ends; sizes whose workspace
+ * (nq_attn_decode_workspace_bytes) exceeds it are refused with
+ * NQ_ERR_WORKSPACE.  The caller still passes every input and output.  All
+ * calls on one GPU share that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race.  Results are those of
+ * nq_attn_decode_paged_fwd with the same arguments.
+ */
+#define NQ_DECODE_SCRATCH_BYTES (16ll << 20)
+int nq_attn_decode_paged_fwd_noalloc(const void* q, const int64_t* q_strides, const void* k_new,
+                                     const int64_t* k_new_strides, const void* v_new,
+                                     const int64_t* v_new_strides, const float* k_weight,
+                                     void* k_pool, const int64_t* k_pool_strides, void* v_pool,
+                                     const int64_t* v_pool_strides, const int32_t* block_table,
+                                     int64_t bt_stride, int page_size, const int32_t* lens,
+                                     int32_t* lens_out, void* o, const int64_t* o_strides, int B,
+                                     int Hq, int Hkv, int D, int max_len, int chunk, int dtype,
+                                     const float* q_weight, float eps, const float* cos_tab,
+                                     const float* sin_tab, int max_pos, const int32_t* q_pos,
+                                     int q_pos0, float sm_scale, void* stream);
+
+/*
  * Append S rows per sequence to a paged cache: K rows QK-Normed (k_weight,
  * NULL = none) and rotated (cos_tab, NULL = none), V rows copied.  Token s of
  * sequence b becomes row row_base[b] + s (row_base NULL: row0 + s) of that

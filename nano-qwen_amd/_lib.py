@@ -80,6 +80,18 @@ SIGNATURES = {
         _p, _p, _i32,                                # cos, sin, max_pos
         _p, _i32, _f32, _p,                          # q_pos, q_pos0, sm_scale, stream
     ]),
+    "nq_attn_decode_paged_fwd_noalloc": (_i32, [
+        _p, _i64p,                                   # q, q_strides
+        _p, _i64p, _p, _i64p, _p,                    # k_new, v_new (+ strides), k_weight
+        _p, _i64p, _p, _i64p,                        # k_pool, v_pool (+ strides)
+        _p, _i64, _i32,                              # block_table, bt_stride, page_size
+        _p, _p,                                      # lens, lens_out
+        _p, _i64p,                                   # o, o_strides
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, D, max_len, chunk, dtype
+        _p, _f32,                                    # q_weight, eps
+        _p, _p, _i32,                                # cos, sin, max_pos
+        _p, _i32, _f32, _p,                          # q_pos, q_pos0, sm_scale, stream
+    ]),
     "nq_kv_append_paged": (_i32, [
         _p, _i64p, _p, _i64p,                        # k, k_strides, v, v_strides
         _p, _i64p, _p, _i64p,                        # k_pool, v_pool (+ strides)

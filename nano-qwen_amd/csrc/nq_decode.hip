@@ -39,6 +39,8 @@
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
 
+#include <mutex>
+
 namespace nq {
 
 constexpr int DC_THREADS = 256;  // four independent waves
@@ -820,4 +822,77 @@ extern "C" int nq_attn_decode_paged_fwd(const void* q, const int64_t* q_strides,
     p.lens_out = lens_out;
   }
   return p.append ? decode_launch<true, true>(p, D, dtype, stream) : decode_launch<true, false>(p, D, dtype, stream);
+}
+
+// ---------------------------------------------------------------- no allocation
+// nq_attn_decode_paged_fwd for callers that cannot allocate (code under HIP
+// graph capture, serving loops, harnesses that forbid hipMalloc): the
+// workspace is this file-scope device array, one copy per GPU, held until the
+// process ends.  In host code `scratch` only names the symbol; its device
+// address (one per GPU) comes from hipGetSymbolAddress on the first call on
+// each device and is what the kernels receive.  Nothing in the workspace has
+// to start at zero: every partial slot and wave index a launch reads, the
+// same launch wrote.  Calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[NQ_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this GPU's scratch array (resolved once per device, with
+// that device current), or null with the error recorded.
+void* scratch_address(int* rc) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *rc = nq_check_launch(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = nq_fail(NQ_ERR_UNSUPPORTED, "device ordinal %d beyond the %d the scratch table holds", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *rc = nq_fail(NQ_ERR_WORKSPACE, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int nq_attn_decode_paged_fwd_noalloc(
+    const void* q, const int64_t* q_strides, const void* k_new, const int64_t* k_new_strides,
+    const void* v_new, const int64_t* v_new_strides, const float* k_weight, void* k_pool,
+    const int64_t* k_pool_strides, void* v_pool, const int64_t* v_pool_strides, const int32_t* block_table,
+    int64_t bt_stride, int page_size, const int32_t* lens, int32_t* lens_out, void* o,
+    const int64_t* o_strides, int B, int Hq, int Hkv, int D, int max_len, int chunk, int dtype,
+    const float* q_weight, float eps, const float* cos_tab, const float* sin_tab, int max_pos,
+    const int32_t* q_pos, int q_pos0, float sm_scale, void* stream) {
+  nq_clear_error();
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0 || Hq % Hkv || !head_dim_ok(D))
+    return nq_fail(NQ_ERR_INVALID, "invalid sizes (B=%d Hq=%d Hkv=%d D=%d max_len=%d)", B, Hq, Hkv, D, max_len);
+  const int64_t need = dc_workspace(B, Hq, Hkv, D, max_len, chunk);
+  if (need > NQ_DECODE_SCRATCH_BYTES)
+    return nq_fail(NQ_ERR_WORKSPACE,
+                   "these sizes need %lld bytes of workspace, more than the %lld of the static scratch; "
+                   "use nq_attn_decode_paged_fwd with a caller-owned workspace",
+                   (long long)need, (long long)NQ_DECODE_SCRATCH_BYTES);
+  int rc = NQ_OK;
+  void* ws = scratch_address(&rc);
+  if (!ws) return rc;
+  return nq_attn_decode_paged_fwd(q, q_strides, k_new, k_new_strides, v_new, v_new_strides, k_weight, k_pool,
+                                  k_pool_strides, v_pool, v_pool_strides, block_table, bt_stride, page_size, lens,
+                                  lens_out, o, o_strides, ws, NQ_DECODE_SCRATCH_BYTES, B, Hq, Hkv, D, max_len,
+                                  chunk, dtype, q_weight, eps, cos_tab, sin_tab, max_pos, q_pos, q_pos0, sm_scale,
+                                  stream);
 }
