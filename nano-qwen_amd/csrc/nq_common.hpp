@@ -150,6 +150,18 @@ __device__ __forceinline__ void global_load_lds16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
+// Raw buffer descriptor over `bytes` bytes at `base` (stride 0; gfx9 word 3).
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// buffer_load_dwordx4 ... lds: lane t copies 16 bytes from the descriptor's
+// base + soff + voff to LDS at lds + 16*t (lds wave-uniform, through M0).
+// Completion is tracked by vmcnt, like global_load_lds.
+__device__ __forceinline__ void buffer_load_lds16(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 // s_waitcnt vmcnt(0): all of this wave's vector-memory loads (including
 // global_load_lds) have completed.
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x3f70); }
@@ -207,6 +219,18 @@ __device__ __forceinline__ float xor32_sum(float v) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// c + the sum of the 8 bf16 values of v, in fp32, with v_dot2_f32_bf16 against
+// (1, 1): four VALU ops for 8 values, exact products, fp32 sums.
+__device__ __forceinline__ float rowsum_bf16x8(bf16x8 v, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), ones, c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), ones, c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), ones, c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), ones, c, false);
+  return c;
+}
 
 // Sum over groups of LPR = 2, 4 or 8 consecutive lanes with DPP (all VALU).
 template <int LPR>

@@ -28,20 +28,26 @@
 // V^T operand is read from the row-major V tile with ds_read_b64_tr_b16.
 //
 // Memory pipeline: K and V tiles (64 keys) travel HBM -> LDS directly with
-// global_load_lds_dwordx4 (no staging registers, no LDS store instructions).
-// K and V are double-buffered separately and K runs one tile ahead: iteration
-// j issues the loads of K[j+2] and V[j+1], computes S[j+1] = K[j+1] Q^T (its
-// MFMAs overlap the softmax VALU work of tile j) and then O += V[j] P[j].
-// Every load has one full iteration to land; one barrier per tile.
+// global_load_lds_dwordx4 / buffer_load_dwordx4 ... lds (no staging registers,
+// no LDS store instructions).  K and V are double-buffered separately and K
+// runs one tile ahead: iteration j issues the loads of K[j+2] and V[j+1], then
+// one stream of MFMAs: S[j+1] = K[j+1] Q^T (the softmax VALU work of tile j
+// interleaved between them) and O += V[j] P[j] (the row max of S[j+1] between
+// those), every LDS operand read two MFMAs ahead of its use.  Every load has
+// one full iteration to land; one barrier per tile.
 //
 // LDS (64 banks on gfx950): rows are unpadded and their 16-byte chunks are
 // XOR-swizzled by row, so the 16 rows one ds_read_b128 of K touches, and the
 // 4 rows x 64 bytes one transpose read of V touches, fall on distinct banks.
 //
-// Softmax: log2 domain (exp2 with log2(e) folded into the scale).  The
-// running max is only raised when some row's tile max exceeds it by more than
-// 2^8 (then O and l are rescaled); otherwise P values up to 256 accumulate
-// against the stale max.  The final O/l is exact either way.
+// Softmax: log2 domain (sm_scale * log2(e) folded into Q before its bf16
+// rounding).  The score MFMAs start from -m (m = running row max), so exp2
+// takes their output as is; the row sum adds the bf16 P values that feed the
+// PV MFMAs (v_dot2 against ones), so numerator and denominator use the same
+// weights.  The running max is only raised when some row's tile max exceeds
+// it by more than 2^8 (then O, l and the pending scores are shifted);
+// otherwise P values up to 256 accumulate against the stale max.  The final
+// O/l is exact either way.
 // Causal workgroups are issued heaviest (last q-block) first.
 
 #include <type_traits>
@@ -57,6 +63,25 @@ constexpr int PF_MAX_ROWS = 256;
 constexpr int64_t PF_WIDE_MIN_WGS = 2048;  // 8-wave workgroups needed to prefer them
 constexpr int PF_BN = 64;     // keys per tile
 constexpr float PF_RESCALE_LOG2 = 8.0f;
+constexpr int PF_READ_AHEAD = 2;  // LDS operand reads in flight ahead of their MFMA
+
+// LDS reads still in flight when op i of a step's MFMA stream waits for its
+// own: those of ops i+1 .. min(i+pd, nops-1); a K operand (op < nqk) is one
+// ds_read_b128, a V^T operand two transpose reads.
+constexpr int stream_younger(int i, int nops, int nqk, int pd) {
+  int c = 0;
+  const int last = (i + pd < nops - 1) ? i + pd : nops - 1;
+  for (int k = i + 1; k <= last; ++k) c += (k < nqk ? 1 : 2);
+  return c;
+}
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 
 struct PrefillParams {
   const void* q;
@@ -160,10 +185,24 @@ prefill_kernel(PrefillParams p) {
                        int tile) {
     const int lds_w = lds_off + wave * 1024;
     if (tile * PF_BN + PF_BN <= p.T) {
-      const unsigned char* tb = base + (int64_t)tile * PF_BN * row_bytes;
+      if constexpr (NW == 4) {
+        // buffer loads: the tile's base in a scalar descriptor, the lane offset
+        // in one 32-bit VGPR, the instruction's row step as a scalar offset.
+        // At 4 waves (4 loads per tile per wave) this frees the 64-bit
+        // per-instruction address VGPRs that otherwise spill in the loop; at
+        // 8 waves the register allocator then spills the lane offset itself
+        // into the loop instead (measured ~8% slower), so 8 waves keep the
+        // global_load_lds form.
+        const BufRsrc r = make_rsrc(base + (int64_t)tile * PF_BN * row_bytes, (uint32_t)(PF_BN * row_bytes));
 #pragma unroll
-      for (int m = 0; m < Tl::LOADS; ++m)
-        global_load_lds16(tb + m * NW * RPI * row_bytes + off, smem + lds_w + m * NW * 1024);
+        for (int m = 0; m < Tl::LOADS; ++m)
+          buffer_load_lds16(r, smem + lds_w + m * NW * 1024, off, (uint32_t)(m * NW * RPI * row_bytes));
+      } else {
+        const unsigned char* tb = base + (int64_t)tile * PF_BN * row_bytes;
+#pragma unroll
+        for (int m = 0; m < Tl::LOADS; ++m)
+          global_load_lds16(tb + m * NW * RPI * row_bytes + off, smem + lds_w + m * NW * 1024);
+      }
     } else {
       const uint32_t chunk_off = off - (uint32_t)(row0 * row_bytes);
 #pragma unroll
@@ -226,8 +265,13 @@ prefill_kernel(PrefillParams p) {
         }
       }
     }
+    // the softmax scale (times log2 e) rides on Q, so S comes out in log2 units
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) qop[db] = to_bf16x8(xf[db]);
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[db][e] *= p.scale_log2;
+      qop[db] = to_bf16x8(xf[db]);
+    }
   }
 
   // ---- per-lane LDS read offsets (bytes within a tile)
@@ -264,7 +308,26 @@ prefill_kernel(PrefillParams p) {
     }
   };
 
-  float m_i = -INFINITY, l_i = 0.f;
+  // Running row max m_i is kept as the sum of two bf16 values, so that -m_i
+  // enters the score MFMAs exactly: S^T = [1 1 0..] x [-m_hi -m_lo 0..]^T
+  // (one extra MFMA per 32-key block, k-slots 0 and 1) + K Q^T.  Every score
+  // then leaves the MFMA already offset by the row max, and exp2 takes it as is.
+  float m_i = 0.f, l_i = 0.f;
+  bf16x8 ones_op, qaug;
+  {
+    const bf16 one = hh == 0 ? (bf16)1.0f : (bf16)0.0f;
+    const bf16 z = (bf16)0.0f;
+    ones_op = bf16x8{one, one, z, z, z, z, z, z};
+  }
+  // m_i <- m rounded to the nearest hi + lo bf16 pair; qaug <- (-hi, -lo)
+  auto set_max = [&](float m) {
+    const bf16 mh = (bf16)m;
+    const bf16 ml = (bf16)(m - (float)mh);
+    m_i = (float)mh + (float)ml;
+    const bf16 z = (bf16)0.0f;
+    qaug = hh == 0 ? bf16x8{(bf16)(-(float)mh), (bf16)(-(float)ml), z, z, z, z, z, z}
+                   : bf16x8{z, z, z, z, z, z, z, z};
+  };
   floatx16 oacc[NDO];
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) oacc[dd] = floatx16{};
@@ -292,7 +355,10 @@ prefill_kernel(PrefillParams p) {
   };
   // row max of the current tile in log2 units (tile 0 holds key 0 for every
   // row, so it is finite there; later tiles compare against a finite m_i)
-  float mx_cur;
+  // (S0 was computed without the offset: its max sets m_i and is subtracted
+  // here; later tiles carry the offset from their MFMAs.)  mx_cur is the row
+  // max of the next tile to be exponentiated, relative to m_i.
+  float mx_cur = 0.f;
   {
     mask_tile(sA, 0);
     float mx = -INFINITY;
@@ -300,16 +366,18 @@ prefill_kernel(PrefillParams p) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(sA[kb][i], sA[kb][i + 1]));
-    mx_cur = xor32_max(mx) * p.scale_log2;
+    set_max(xor32_max(mx));
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sA[kb] -= m_i;
   }
 
   // One 64-key tile.  Order inside a step: barrier + next loads; rescale
   // against the row max of S[j] (found in the previous step); then one
-  // branch-free block in which the MFMAs of S[j+1] = K[j+1] Q^T are
-  // interleaved with the exp/sum/convert of P[j] (sched_barrier keeps them
-  // interleaved, since a wave issues in order); then, in the steps that may need
-  // it, the mask of S[j+1]; then O += V[j]^T P[j], with the row max of S[j+1]
-  // taken alongside those MFMAs.
+  // fixed-order stream in which the MFMAs of S[j+1] = K[j+1] Q^T are
+  // interleaved with the exp/pack/sum of P[j] (sched_barrier keeps them
+  // interleaved, since a wave issues in order); then, in the steps that may
+  // need it, the mask of S[j+1]; then O += V[j]^T P[j], with the row max of
+  // S[j+1] taken alongside those MFMAs.
   auto step = [&](auto parity, auto has_next, auto may_mask, int j) {
     constexpr int P = decltype(parity)::value;       // == j & 1
     constexpr bool NEXT = decltype(has_next)::value;  // j + 1 < ntiles
@@ -328,95 +396,94 @@ prefill_kernel(PrefillParams p) {
 
     // online softmax (log2 domain); each lane owns one query row
     (void)n0;
-    if (wave_any(mx_cur > m_i + PF_RESCALE_LOG2)) {
-      const float m_new = fmaxf(m_i, mx_cur);
-      const float alpha = fast_exp2(m_i - m_new);  // 0 on the first tile
+    if (wave_any(mx_cur > PF_RESCALE_LOG2)) {
+      const float m_old = m_i;
+      set_max(m_i + fmaxf(mx_cur, 0.f));
+      const float delta = m_i - m_old;
+      const float alpha = fast_exp2(-delta);
       l_i *= alpha;
 #pragma unroll
       for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
-      m_i = m_new;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) s_cur[kb] -= delta;
     }
 
-    // ---- branch-free block, issued in a fixed order (sched_barrier fences)
-    // Phase B: NDB steps; step db reads the K operands of step db+1, issues
-    // the two MFMAs of S[j+1] for k-block db and computes 32/NDB of this
-    // lane's P values (exp2, row sum, bf16 pack) while those MFMAs run.
-    constexpr int PER = 32 / NDB;  // P values per step
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // ---- one fixed-order stream of MFMAs (sched_barrier fences; a wave
+    // issues in order).  Op i < NQK: S[j+1] for k-block i/2, key half i%2
+    // (A = K[j+1] from LDS, B = Q), after one op that loads -m_i into both
+    // halves' accumulators; op NQK + t: O^T[t % NDO] += V[j]^T (keys 16*(t/NDO)..)
+    // P[j]^T.  LDS operands are read PD ops ahead (K: one ds_read_b128, V^T:
+    // two transpose reads), issued as inline asm so the HBM->LDS loads just
+    // issued keep flying (the compiler would wait for them before an LDS read
+    // it can see), with lgkmcnt counting this stream's reads only.  Between
+    // the QK MFMAs go the exp2 / bf16 pack / row sum of P[j] (two values per
+    // op), between the PV MFMAs the row max of S[j+1].
+    constexpr int NQK = NEXT ? 2 * NDB : 0;
+    constexpr int NPV = 4 * NDO;
+    constexpr int NOPS = NQK + NPV;
+    constexpr int PD = PF_READ_AHEAD;
+    const uint32_t Kt = lds_addr(smem + (P ^ 1) * TB);
+    const uint32_t Vt = lds_addr(smem + (2 + P) * TB);
+    float acc[2] = {0.f, 0.f};
     floatx8 tv[4];
     bf16x8 pop[4];
-    bf16x8 ka0, ka1, kn0, kn1;
-    floatx16 sn0 = floatx16{}, sn1 = floatx16{};
-    const unsigned char* Kn = smem + (P ^ 1) * TB;
-    if (NEXT) {
-      ka0 = *reinterpret_cast<const bf16x8*>(Kn + k_off[0]);
-      ka1 = *reinterpret_cast<const bf16x8*>(Kn + k_off[0] + 32 * Tl::ROW_BYTES);
-    }
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      if (NEXT) {
-        if (db + 1 < NDB) {
-          kn0 = *reinterpret_cast<const bf16x8*>(Kn + k_off[db + 1]);
-          kn1 = *reinterpret_cast<const bf16x8*>(Kn + k_off[db + 1] + 32 * Tl::ROW_BYTES);
-        }
-        sn0 = mfma32(ka0, qop[db], sn0);
-        sn1 = mfma32(ka1, qop[db], sn1);
-      }
-#pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        const int idx = db * PER + u;  // 0..31: (kb, element)
-        const float pe = fast_exp2(s_cur[idx / 16][idx % 16] * p.scale_log2 - m_i);
-        acc[idx / 8] += pe;
-        tv[idx / 8][idx % 8] = pe;
-        if (idx % 8 == 7) pop[idx / 8] = to_bf16x8(tv[idx / 8]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (NEXT) {
-        ka0 = kn0;
-        ka1 = kn1;
-      }
-    }
-    if (NEXT) {
-      s_next[0] = sn0;
-      s_next[1] = sn1;
-    }
-    l_i += (acc[0] + acc[1]) + (acc[2] + acc[3]);
-
-    // Phase C: O^T += V[j]^T P^T, next transpose-read operand prefetched.
-    // V[j] landed before this step's barrier; the reads are issued as inline
-    // asm so the loads just issued for K[j+2] / V[j+1] keep flying through
-    // this phase (the builtin would wait for them).  No other LDS access is
-    // outstanding here, so lgkmcnt(2) means "all but the two newest reads".
-    const uint32_t Vt = lds_addr(smem + (2 + P) * TB);
-    auto vread = [&](int idx) {
-      return lds_read_tr8_nowait<8 * D>(Vt + v_off[idx % NDO] + (idx / NDO) * 16 * Tl::ROW_BYTES);
-    };
-    if (NEXT && MASKN) mask_tile(s_next, n0 + PF_BN);  // diagonal / last tiles only
-    constexpr int NPV = 4 * NDO;        // PV MFMAs
-    constexpr int MPER = 32 / NPV;      // S[j+1] elements folded into the max per MFMA
+    bf16x8 opnd[PD + 1];
+    floatx16 sn[2];
     float mxn = -INFINITY;
-    bf16x8 va = vread(0);
-#pragma unroll
-    for (int idx = 0; idx < NPV; ++idx) {
-      bf16x8 vn;
-      if (idx + 1 < NPV) {
-        vn = vread(idx + 1);
-        lgkm_wait<2>();
+    auto issue = [&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if constexpr (i < NQK) {
+        opnd[i % (PD + 1)] = lds_read_b128_nowait<(i % 2) * 32 * Tl::ROW_BYTES>(Kt + k_off[i / 2]);
       } else {
-        lgkm_wait<0>();
+        constexpr int t = i - NQK;
+        opnd[i % (PD + 1)] = lds_read_tr8_nowait<8 * D>(Vt + v_off[t % NDO] + (t / NDO) * 16 * Tl::ROW_BYTES);
       }
-      oacc[idx % NDO] = mfma32(va, pop[idx / NDO], oacc[idx % NDO]);
-      if (NEXT) {
+    };
+    // P[j] values e: exp2, and per 8 values a bf16 pack and its row sum
+    auto pwork = [&](int e) {
+      tv[e / 8][e % 8] = fast_exp2(s_cur[e / 16][e % 16]);
+      if (e % 8 == 7) {
+        pop[e / 8] = to_bf16x8(tv[e / 8]);
+        acc[(e / 8) & 1] = rowsum_bf16x8(pop[e / 8], acc[(e / 8) & 1]);
+      }
+    };
+    static_for<0, (PD < NOPS ? PD : NOPS)>(issue);
+    floatx16 s_init;  // -m_i in every element; the first MFMA of each key half starts from it
+    if (NEXT) s_init = mfma32(ones_op, qaug, floatx16{});
+    if (NQK == 0) {  // last tile: all of P[j] before the PV stream
 #pragma unroll
-        for (int u = 0; u < MPER; ++u) {
-          const int e = idx * MPER + u;
-          mxn = fmaxf(mxn, s_next[e / 16][e % 16]);
+      for (int e = 0; e < 32; ++e) pwork(e);
+    }
+    static_for<0, NOPS>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if constexpr (i + PD < NOPS) issue(std::integral_constant<int, i + PD>{});
+      lgkm_wait<stream_younger(i, NOPS, NQK, PD)>();
+      if constexpr (i < NQK) {
+        sn[i % 2] = mfma32(opnd[i % (PD + 1)], qop[i / 2], i < 2 ? s_init : sn[i % 2]);
+        constexpr int per = NQK ? 32 / NQK : 1;  // P values per QK op
+#pragma unroll
+        for (int u = 0; u < per; ++u) pwork(i * per + u);
+      } else {
+        constexpr int t = i - NQK;
+        if constexpr (t == 0 && NEXT) {
+          s_next[0] = sn[0];
+          s_next[1] = sn[1];
+          if (MASKN) mask_tile(s_next, n0 + PF_BN);  // diagonal / last tiles only
+        }
+        oacc[t % NDO] = mfma32(opnd[i % (PD + 1)], pop[t / NDO], oacc[t % NDO]);
+        if (NEXT) {
+          constexpr int mper = 32 / NPV;  // S[j+1] elements folded into the max per op
+#pragma unroll
+          for (int u = 0; u < mper; ++u) {
+            const int e = t * mper + u;
+            mxn = fmaxf(mxn, s_next[e / 16][e % 16]);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (idx + 1 < NPV) va = vn;
-    }
-    if (NEXT) mx_cur = xor32_max(mxn) * p.scale_log2;
+    });
+    l_i += acc[0] + acc[1];
+    if (NEXT) mx_cur = xor32_max(mxn);
   };
 
   using I0 = std::integral_constant<int, 0>;

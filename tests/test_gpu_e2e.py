@@ -224,7 +224,11 @@ def test_fixed_semantics_cache_matches_nocache(gold, model):
     finally:
         model.set_cache_semantics(False)
     torch.testing.assert_close(pre.float(), full[:-1].float(), atol=0.05, rtol=0)
-    torch.testing.assert_close(dec.float(), full[-1].float(), atol=0.05, rtol=0)
+    # The last row comes from the decode kernel (fp32 P against bf16 V) on one
+    # side and the prefill kernel (bf16 P on the MFMA) on the other; through the
+    # bf16 model's layers their logits differ by a few bf16 steps (0.0625 at
+    # |logit| >= 8).  A cache or position mistake moves logits by O(1).
+    torch.testing.assert_close(dec.float(), full[-1].float(), atol=0.1, rtol=0)
 
 
 def test_training_step_gradients_against_oracle(weights):
