@@ -12,8 +12,10 @@
  *     sequence) axes; the head_dim axis must be contiguous.  Base pointers must
  *     be 16-byte aligned and strides multiples of 16 bytes.
  *   - dtype codes: NQ_DTYPE_BF16 (bfloat16 stored as 16-bit words) or
- *     NQ_DTYPE_F32.  Matrix products run on bf16 MFMA with fp32 accumulation;
- *     norm, RoPE and softmax arithmetic is fp32.
+ *     NQ_DTYPE_F32.  bf16 data: matrix products on bf16 MFMA with fp32
+ *     accumulation.  fp32 data in nq_attn_prefill_fwd: products on fp32 MFMA
+ *     (the reference's SDPA keeps the input dtype).  Norm, RoPE and softmax
+ *     arithmetic is fp32 everywhere.
  *   - head_dim must be 32, 64 or 128 (the reference's configs use 32 and 128;
  *     kernels/flash_attn.py:106 also allows 16 and 256, which are refused
  *     here with NQ_ERR_UNSUPPORTED).  num_heads % num_kv_heads == 0 and query
@@ -105,11 +107,10 @@ int nq_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, void* y,
  * already normalised and rotated by nq_qk_norm_rope, V raw), the GQA
  * expansion of attention.py:106-108 is implicit, and SDPA is replaced.
  *
- * q: (B, Hq, S, D) with strides q_strides; k, v: (B, Hkv, T, D), always
- *   bf16 (their tiles are copied into LDS unconverted; callers holding fp32
- *   K/V convert them first); o: output (B, Hq, S, D) with strides o_strides
- *   (pass the strides of a (B, S, Hq, D) buffer to get o_proj's input layout
- *   directly).  q and o use `dtype`.
+ * q: (B, Hq, S, D) with strides q_strides; k, v: (B, Hkv, T, D); o: output
+ *   (B, Hq, S, D) with strides o_strides (pass the strides of a (B, S, Hq, D)
+ *   buffer to get o_proj's input layout directly).  q, k, v and o all use
+ *   `dtype`; NQ_DTYPE_F32 runs every product in fp32 (v_mfma_f32_32x32x2_f32).
  * lse: optional fp32 (B, Hq, S) natural-log sum-exp of the scaled scores.
  * q_weight: RMSNorm weight for Q (NULL = none); cos_tab/sin_tab: RoPE table
  *   for Q (NULL = none); q_pos / q_pos_base / q_pos0: Q positions as in
@@ -117,7 +118,8 @@ int nq_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, void* y,
  * causal: query i sees key j iff j <= i + (T - S) (top-left == bottom-right
  *   when S == T, which is SDPA's is_causal in the reference).
  * sm_scale <= 0 selects 1/sqrt(D), SDPA's default (attention.py:110).
- * Requires 256 % (Hq / Hkv) == 0 and S <= T when causal.
+ * Requires 256 % (Hq / Hkv) == 0 (fp32: 128 % (Hq / Hkv) == 0) and S <= T
+ * when causal.
  */
 int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides,
@@ -289,8 +291,9 @@ int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S);
  * dq (B, Hq, S, D), dk / dv (B, Hkv, T, D): outputs, fully written.
  * causal keeps key j for query i iff j <= i + T - S (needs S <= T).
  * workspace: nq_attn_bwd_workspace_bytes(B, Hq, S) bytes.
- * Requires 128 % (Hq / Hkv) == 0.  Storage dtype bf16 or fp32 (products on
- * bf16 MFMA, accumulation and softmax in fp32).
+ * Requires 128 % (Hq / Hkv) == 0.  Storage dtype bf16 (products on bf16
+ * MFMA) or fp32 (products on fp32 MFMA, as the reference's fp32 autograd);
+ * accumulation and softmax in fp32 either way.
  */
 int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,

@@ -33,31 +33,12 @@
 
 #include <type_traits>
 
+#include "nq_backward.hpp"
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
 
 namespace nq {
 
-struct BwdParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  const void* o;
-  const void* dout;
-  const float* lse;  // (B, Hq, S) natural log
-  // scratch written by bwd_dq_kernel: per (batch, head) and 32-row query
-  // tile, 64 floats = [32 x LSE * log2(e) | 32 x Delta], rows past S zero
-  float* ws;
-  int nst;           // 32-row tiles per (batch, head)
-  void* dq;
-  void* dk;
-  void* dv;
-  int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss;
-  int64_t osb, osh, oss, dosb, dosh, doss;
-  int64_t dqsb, dqsh, dqss, dksb, dksh, dkss, dvsb, dvsh, dvss;
-  int B, Hq, Hkv, G, S, T, BM, nqb, coff;
-  float scale, scale_log2;
-};
 
 constexpr int BW_BN = 64;     // keys per tile (dQ kernel)
 constexpr int BW_BQ = 32;     // query rows per tile (dK/dV kernel)
@@ -81,9 +62,6 @@ struct BwTile {
 
 // ---------------------------------------------------------------- scratch
 // Index of (batch b, head h, query s) in the scratch: its LSE; Delta is 32 on.
-__device__ __forceinline__ int64_t bw_ws_index(const BwdParams& p, int b, int h, int s) {
-  return (((int64_t)b * p.Hq + h) * p.nst + s / 32) * 64 + (s & 31);
-}
 
 // Stage a tile of NR rows (rows >= nvalid clamp to the last valid row; their
 // scores are masked) into LDS, swizzled.  bf16 storage: global_load_lds
@@ -725,18 +703,17 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   // dQ workgroups: 8 waves (256 query rows: each K/V tile load serves twice
   // the rows) when that still gives enough workgroups to fill the device
   const int64_t wide_wgs = (int64_t)B * Hkv * ((S + 256 / G - 1) / (256 / G));
-  const int nw = wide_wgs >= BW_DQ_WIDE_MIN_WGS ? 8 : 4;
+  const bool f32 = dtype == NQ_DTYPE_F32;  // fp32 tensors: the fp32 MFMA kernels (4 waves)
+  const int nw = (!f32 && wide_wgs >= BW_DQ_WIDE_MIN_WGS) ? 8 : 4;
   p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
   p.coff = T - S;
   p.scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = p.scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (dtype == NQ_DTYPE_BF16)
-    e = with_head_dim(D, [&](auto dc) { return launch_bwd<decltype(dc)::value, bf16>(p, nw, causal != 0, st); });
-  else
-    e = with_head_dim(D, [&](auto dc) { return launch_bwd<decltype(dc)::value, float>(p, nw, causal != 0, st); });
+  if (f32) return nq_check_launch(launch_bwd_f32(p, D, causal != 0, st));
+  const hipError_t e =
+      with_head_dim(D, [&](auto dc) { return launch_bwd<decltype(dc)::value, bf16>(p, nw, causal != 0, st); });
   return nq_check_launch(e);
 }
 

@@ -54,6 +54,7 @@
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
+#include "nq_prefill.hpp"
 
 namespace nq {
 
@@ -83,27 +84,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-struct PrefillParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* o;
-  float* lse;
-  int64_t qsb, qsh, qss;
-  int64_t ksb, ksh, kss;
-  int64_t vsb, vsh, vss;
-  int64_t osb, osh, oss;
-  const float* qw;
-  float eps;
-  const float* cos_tab;
-  const float* sin_tab;
-  int max_pos;
-  const int32_t* q_pos;
-  const int32_t* q_pos_base;
-  int q_pos0;
-  int B, Hq, Hkv, G, S, T, BM, nqb;
-  float scale_log2;  // sm_scale * log2(e)
-};
 
 // MFMA row r of a 32-key block holds key sigma(r): bits 2 and 3 swapped.
 __device__ __forceinline__ int key_perm32(int r) {
@@ -569,6 +549,8 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d S=%d T=%d)", B, Hq, Hkv, S, T);
   if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
   const int G = Hq / Hkv;
+  const bool f32 = dtype == NQ_DTYPE_F32;  // fp32 q, k, v, o: the fp32 MFMA kernel
+  if (f32 && 128 % G) return nq_fail(NQ_ERR_UNSUPPORTED, "fp32: GQA group size %d must divide 128", G);
   if (PF_MAX_ROWS % G) return nq_fail(NQ_ERR_UNSUPPORTED, "GQA group size %d must divide %d", G, PF_MAX_ROWS);
   if (D == 32 && 128 % G)
     return nq_fail(NQ_ERR_UNSUPPORTED, "at head_dim 32 the GQA group size %d must divide 128", G);
@@ -578,16 +560,12 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   if (!nq_aligned16(q) || !nq_aligned16(k) || !nq_aligned16(v) || !nq_aligned16(o))
     return nq_fail(NQ_ERR_INVALID, "base pointers must be 16-byte aligned");
   const int esz = nq_dtype_size(dtype);
-  for (const int64_t* s : {q_strides, o_strides})
+  for (const int64_t* s : {q_strides, k_strides, v_strides, o_strides})
     for (int i = 0; i < 3; ++i)
-      if ((s[i] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "q/o strides must be multiples of 16 bytes");
-  for (const int64_t* s : {k_strides, v_strides}) {  // bf16 rows
-    for (int i = 0; i < 3; ++i)
-      if ((s[i] * 2) % 16) return nq_fail(NQ_ERR_INVALID, "k/v strides must be multiples of 16 bytes");
-    // a tile's lane offsets (64 rows) are 32-bit
-    if (s[2] < 0 || (int64_t)PF_BN * s[2] * 2 >= (1LL << 31))
+      if ((s[i] * esz) % 16) return nq_fail(NQ_ERR_INVALID, "strides must be multiples of 16 bytes");
+  for (const int64_t* s : {k_strides, v_strides})  // a bf16 tile's lane offsets (64 rows) are 32-bit
+    if (s[2] < 0 || (int64_t)PF_BN * s[2] * esz >= (1LL << 31))
       return nq_fail(NQ_ERR_UNSUPPORTED, "k/v sequence stride %lld too large", (long long)s[2]);
-  }
   if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
   PrefillParams p{};
@@ -599,6 +577,15 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   p.qw = q_weight; p.eps = eps; p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
   p.q_pos = q_pos; p.q_pos_base = q_pos_base; p.q_pos0 = q_pos0;
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
+  const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
+  p.scale_log2 = scale * kLog2e;
+  const bool fuse = q_weight != nullptr || cos_tab != nullptr;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (f32) {
+    p.BM = 128 / G;
+    p.nqb = (S + p.BM - 1) / p.BM;
+    return nq_check_launch(launch_prefill_f32(p, D, causal != 0, fuse, st));
+  }
   // 256 rows per workgroup when that still gives enough workgroups, else 128
   const int64_t wide_wgs = (int64_t)B * Hkv * ((S + PF_MAX_ROWS / G - 1) / (PF_MAX_ROWS / G));
   // (a D = 32 tile is 4 KiB: one 1 KiB load per wave of a 4-wave workgroup,
@@ -606,14 +593,7 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   const int nw = (128 % G == 0 && (wide_wgs < PF_WIDE_MIN_WGS || D == 32)) ? 4 : 8;
   p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
-  const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
-  p.scale_log2 = scale * kLog2e;
-  const bool fuse = q_weight != nullptr || cos_tab != nullptr;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (dtype == NQ_DTYPE_BF16)
-    e = with_head_dim(D, [&](auto dc) { return launch_prefill<decltype(dc)::value, bf16>(p, nw, causal, fuse, st); });
-  else
-    e = with_head_dim(D, [&](auto dc) { return launch_prefill<decltype(dc)::value, float>(p, nw, causal, fuse, st); });
+  const hipError_t e =
+      with_head_dim(D, [&](auto dc) { return launch_prefill<decltype(dc)::value, bf16>(p, nw, causal, fuse, st); });
   return nq_check_launch(e);
 }

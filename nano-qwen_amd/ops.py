@@ -282,10 +282,6 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise TypeError("q, k and v must share one dtype")
     dt = _code(q)
-    # the kernel streams bf16 K/V tiles into LDS as they are stored; fp32 K/V
-    # (the fp32 module path) are rounded to bf16 here, as the MFMAs would anyway
-    if k.dtype != torch.bfloat16:
-        k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
     q, k, v = _rows_in(q), _rows_in(k), _rows_in(v)
     if out is None:
         out = torch.empty(B, S, Hq, D, dtype=q.dtype, device=q.device).transpose(1, 2)

@@ -5,9 +5,10 @@ functions (``attention``, ``rms_norm``, ``rotate_half``, pinned by the
 oracle tests), on the same bf16-valued (or fp32) inputs.
 
 Tolerance for gradients, relative to the largest reference magnitude of the
-same tensor: max-abs <= 2e-2 * max|ref| and mean-abs <= 2e-3 * max|ref| (the
-bf16 gate of the forward, scaled to the tensor), for bf16 and fp32 storage
-alike, since the products run on bf16 MFMA either way.
+same tensor: bf16 storage max-abs <= 2e-2 * max|ref| and mean-abs <=
+2e-3 * max|ref| (the bf16 gate of the forward, scaled to the tensor); fp32
+storage, whose products run on fp32 MFMA, max-abs <= 1e-5 * max|ref| and
+mean-abs <= 1e-6 * max|ref|.
 """
 
 import pytest
@@ -23,10 +24,11 @@ DEV = "cuda"
 
 
 def _close_rel(got, ref, what, dtype=torch.bfloat16):
+    assert got.dtype == dtype, f"{what}: {got.dtype} result for {dtype} inputs"
     got = got.detach().double().cpu()
     ref = ref.detach().double().cpu()
     scale = float(ref.abs().max())
-    mx_tol, mean_tol = 2e-2, 2e-3
+    mx_tol, mean_tol = (1e-5, 1e-6) if dtype == torch.float32 else (2e-2, 2e-3)
     d = (got - ref).abs()
     assert torch.isfinite(got).all(), f"{what}: non-finite values"
     assert float(d.max()) <= mx_tol * scale and float(d.mean()) <= mean_tol * scale, \
@@ -71,11 +73,29 @@ def test_attention_backward_bottom_right_causal_and_dtypes(dtype):
     do = randn(B, Hq, S, D, seed=514, dtype=dtype)
     o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, return_lse=True)
     dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=True)
-    # the kernels round fp32 K/V (and the MFMA operands) to bf16: the reference sees the same rounding
-    kr, vr = (k.bfloat16().to(dtype), v.bfloat16().to(dtype)) if dtype == torch.float32 else (k, v)
-    _, rq, rk, rv = _ref_grads(q, kr, vr, do, True)
+    _, rq, rk, rv = _ref_grads(q, k, v, do, True)
     for got, ref, name in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
         _close_rel(got, ref, name, dtype)
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("Hq,Hkv,S,T,causal", [(4, 4, 200, 200, True), (8, 2, 77, 301, True),
+                                                (16, 1, 130, 130, False), (8, 8, 257, 64, False)])
+def test_fp32_attention_backward(D, Hq, Hkv, S, T, causal):
+    """fp32 storage runs the fp32 MFMA backward: every gradient at the fp32 gate
+    against fp64 autograd, the forward's O and LSE from the fp32 prefill."""
+    say(f"bwd fp32 D={D} {Hq}/{Hkv} S={S} T={T} causal={causal}")
+    B = 2
+    q = randn(B, Hq, S, D, seed=581 + D)
+    k = randn(B, Hkv, T, D, seed=582 + D)
+    v = randn(B, Hkv, T, D, seed=583 + D)
+    do = randn(B, Hq, S, D, seed=584 + D)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=causal)
+    ro, rq, rk, rv = _ref_grads(q, k, v, do, causal)
+    _close_rel(o, ro, "o", torch.float32)
+    for got, ref, name in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+        _close_rel(got, ref, name, torch.float32)
 
 
 def test_attention_backward_long_sequence():

@@ -235,9 +235,10 @@ def test_training_step_gradients_against_oracle(weights):
     """One cross-entropy training step of the fp32 model on the kernels (attention
     forward and backward: prefill with LSE, the FlashAttention-2 backward, the
     QK-Norm + RoPE backward), every parameter gradient against fp64 autograd
-    through the oracle model.  Gate per tensor, relative to its largest reference
-    magnitude: max-abs <= 2e-2 and mean-abs <= 2e-3 (the products run on bf16
-    MFMA)."""
+    through the oracle model.  The fp32 model's attention runs its products on
+    fp32 MFMA, so the gate is fp32-level: loss within 1e-5 relative, and per
+    tensor, relative to its largest reference magnitude, max-abs <= 1e-4 and
+    mean-abs <= 1e-5 (a few layers of fp32 rounding against fp64)."""
     say("training step gradients (kernels vs oracle fp64 autograd)")
     torch.manual_seed(0)
     m = Qwen3Model(ModelConfig(**MODEL)).train()
@@ -256,8 +257,9 @@ def test_training_step_gradients_against_oracle(weights):
                                              ids[:, 1:].reshape(-1))
     loss.backward()
     got_loss, ref_loss = out["loss"].detach().item(), loss.detach().item()
-    assert abs(got_loss - ref_loss) <= 1e-2 * ref_loss, (got_loss, ref_loss)
+    assert abs(got_loss - ref_loss) <= 1e-5 * ref_loss, (got_loss, ref_loss)
     grads = dict(m.named_parameters())
+    worst = 0.0
     for name, ref in ref_w.items():
         got = grads[name].grad
         assert got is not None, name
@@ -265,5 +267,7 @@ def test_training_step_gradients_against_oracle(weights):
         r = ref.grad
         scale = float(r.abs().max())
         d = (got - r).abs()
-        assert float(d.max()) <= 2e-2 * scale and float(d.mean()) <= 2e-3 * scale, \
+        worst = max(worst, float(d.max()) / scale)
+        assert float(d.max()) <= 1e-4 * scale and float(d.mean()) <= 1e-5 * scale, \
             f"{name}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {scale:.3e})"
+    say(f"training step: loss rel err {abs(got_loss - ref_loss) / ref_loss:.2e}, worst grad rel err {worst:.2e}")

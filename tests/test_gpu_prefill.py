@@ -5,7 +5,7 @@ import torch
 
 import nano_qwen_amd as nq
 from oracle import attention, attention_path, rms_norm, rope_tables, rotate_half
-from tests.helpers import assert_bf16_close, randn, say
+from tests.helpers import assert_bf16_close, assert_close_for, assert_fp32_close, randn, say
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -59,7 +59,34 @@ def test_debug_scale_config(dtype):
     ref = attention_path(q.float(), k.float(), v.float(), q_weight=ones, k_weight=ones, eps=1e-6,
                          cos=cos, sin=sin, q_pos=torch.arange(256), causal=True)
     assert o.dtype == dtype
-    assert_bf16_close(o, ref, "debug config")
+    assert_close_for(dtype, o, ref, "debug config")
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("Hq,Hkv,S,causal", [(8, 2, 256, True), (4, 4, 77, True), (16, 1, 130, False),
+                                              (32, 4, 33, True), (8, 8, 1, True)])
+def test_fp32_prefill(D, Hq, Hkv, S, causal):
+    """fp32 inputs run the fp32 MFMA kernel: QK-Norm + RoPE + GQA attention at the fp32 gate."""
+    say(f"prefill fp32 D={D} Hq={Hq} Hkv={Hkv} S={S} causal={causal}")
+    o, ref = run_case(2, S, Hq, Hkv, D, torch.float32, seed=300 + D + S, causal=causal)
+    assert_fp32_close(o, ref, f"fp32 D={D} G={Hq // Hkv} S={S}")
+
+
+def test_fp32_queries_after_cached_keys_and_lse():
+    """fp32, S < T (bottom-right causal) with the log-sum-exp output."""
+    say("prefill fp32 S<T + lse")
+    B, S, T, Hq, Hkv, D = 2, 45, 203, 8, 2, 64
+    q = randn(B, Hq, S, D, seed=61)
+    k = randn(B, Hkv, T, D, seed=62)
+    v = randn(B, Hkv, T, D, seed=63)
+    o, lse = nq.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, return_lse=True)
+    ref = attention(q.float(), k.float(), v.float(), causal=True, causal_offset=T - S)
+    assert_fp32_close(o, ref, "fp32 S<T")
+    s = torch.matmul(q, k.repeat_interleave(Hq // Hkv, 1).transpose(-1, -2))
+    s = s / D ** 0.5
+    keep = torch.ones(S, T, dtype=torch.bool).tril(T - S)
+    s = s.masked_fill(~keep, float("-inf"))
+    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=0, atol=1e-5)
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(4, 4), (16, 8), (32, 8), (32, 4), (32, 2)])
