@@ -38,6 +38,7 @@
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
+#include "nq_prefill.hpp"
 
 #include <mutex>
 
@@ -721,14 +722,85 @@ static int decode_setup(DecodeParams& p, const void* q, const int64_t* q_strides
   return NQ_OK;
 }
 
+// ---------------------------------------------------------------- fp32 caches
+// An fp32 cache keeps fp32 arithmetic (the reference's SDPA runs in the input
+// dtype): the append, when fused, is its own launch, then the fp32 MFMA
+// attention kernel of the prefill runs with S = 1 over each sequence's keys
+// (its per-sequence lengths and block table), with the same length, position
+// and NaN rules as the bf16 path.  The workspace is not used.
+
+// The new token's K (QK-Normed with kw, rotated at the query's position) and
+// V to row lens[b] of the paged cache, and lens_out[b] = lens[b] + 1; a
+// sequence whose length is out of range appends nothing and keeps lens[b].
+// D/16 lanes per (batch, kv head) row, as the row kernel.
+template <int D>
+__global__ void __launch_bounds__(256) decode_append_f32_kernel(DecodeParams p) {
+  constexpr int LPR = D / 16;
+  const int64_t gl = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gl / LPR;  // whole groups of LPR lanes leave together
+  const int sub = (int)(gl % LPR);
+  if (row >= (int64_t)p.B * p.Hkv) return;
+  const int b = (int)(row / p.Hkv), kvh = (int)(row % p.Hkv);
+  const int len = batch_len(p, b);
+  if (kvh == 0 && sub == 0 && p.lens_out) p.lens_out[b] = len < 0 ? p.lens[b] : p.lens[b] + 1;
+  if (len < 0) return;
+  const int t = len - 1;  // the new key's row
+  const int pos = table_row(p.q_pos ? p.q_pos[b] : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos);
+  const float* kn = reinterpret_cast<const float*>(p.kn) + b * p.knsb + kvh * p.knsh;
+  const float* vn = reinterpret_cast<const float*>(p.vn) + b * p.vnsb + kvh * p.vnsh;
+  floatx8 x1 = Vec8<float>::load_f32(kn + sub * 8), x2 = Vec8<float>::load_f32(kn + D / 2 + sub * 8);
+  floatx8 w1, w2;
+  if (p.kw) {
+    w1 = Vec8<float>::load_f32(p.kw + sub * 8);
+    w2 = Vec8<float>::load_f32(p.kw + D / 2 + sub * 8);
+  }
+  norm_rope_row<D>(x1, x2, p.kw ? &w1 : nullptr, &w2, p.eps, p.cos_tab, p.sin_tab, pos, sub);
+  const int64_t pg = p.bt[b * p.bts + t / p.page];
+  float* kd = reinterpret_cast<float*>(p.kc) + pg * p.ksb + kvh * p.ksh + (int64_t)(t % p.page) * p.kst;
+  float* vd = reinterpret_cast<float*>(p.vc) + pg * p.vsb + kvh * p.vsh + (int64_t)(t % p.page) * p.vst;
+  store8<float>(kd + sub * 8, x1);
+  store8<float>(kd + D / 2 + sub * 8, x2);
+  store8<float>(vd + sub * 8, Vec8<float>::load_f32(vn + sub * 8));
+  store8<float>(vd + D / 2 + sub * 8, Vec8<float>::load_f32(vn + D / 2 + sub * 8));
+}
+
+static int decode_launch_f32(const DecodeParams& d, int D, bool paged, bool append, void* stream) {
+  if (128 % d.G) return nq_fail(NQ_ERR_UNSUPPORTED, "fp32 decode: GQA group size %d must divide 128", d.G);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (append) {
+    const int64_t threads = (int64_t)d.B * d.Hkv * (D / 16);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    with_head_dim(D, [&](auto dc) {
+      hipLaunchKernelGGL((decode_append_f32_kernel<decltype(dc)::value>), grid, dim3(256), 0, st, d);
+      return 0;
+    });
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return nq_check_launch(e);
+  }
+  PrefillParams p{};
+  p.q = d.q; p.qsb = d.qsb; p.qsh = d.qsh; p.qss = 0;
+  p.k = d.kc; p.ksb = d.ksb; p.ksh = d.ksh; p.kss = d.kst;
+  p.v = d.vc; p.vsb = d.vsb; p.vsh = d.vsh; p.vss = d.vst;
+  p.o = d.o; p.osb = d.osb; p.osh = d.osh; p.oss = 0;
+  p.qw = d.qw; p.eps = d.eps; p.cos_tab = d.cos_tab; p.sin_tab = d.sin_tab; p.max_pos = d.max_pos;
+  p.q_pos = d.q_pos;
+  // no lens: every sequence holds max_len keys, the query at max_len - 1
+  p.q_pos0 = (!d.lens && !d.q_pos && d.q_pos0 < 0) ? d.max_len - 1 : d.q_pos0;
+  p.B = d.B; p.Hq = d.Hq; p.Hkv = d.Hkv; p.G = d.G; p.S = 1; p.T = d.max_len;
+  p.BM = 128 / d.G; p.nqb = 1;
+  p.scale_log2 = d.scale_log2;
+  p.kv_lens = d.lens; p.kv_extra = d.append; p.kv_max = d.max_len;
+  if (paged) { p.bt = d.bt; p.bts = d.bts; p.page = d.page; }
+  const bool fuse = d.qw != nullptr || d.cos_tab != nullptr;
+  return nq_check_launch(launch_prefill_f32(p, D, false, fuse, st));
+}
+
 template <bool PAGED, bool APPEND>
 static int decode_launch(const DecodeParams& p, int D, int dtype, void* stream) {
+  if (dtype == NQ_DTYPE_F32) return decode_launch_f32(p, D, PAGED, APPEND, stream);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (dtype == NQ_DTYPE_BF16)
-    e = with_head_dim(D, [&](auto dc) { return launch_decode<decltype(dc)::value, bf16, PAGED, APPEND>(p, st); });
-  else
-    e = with_head_dim(D, [&](auto dc) { return launch_decode<decltype(dc)::value, float, PAGED, APPEND>(p, st); });
+  const hipError_t e =
+      with_head_dim(D, [&](auto dc) { return launch_decode<decltype(dc)::value, bf16, PAGED, APPEND>(p, st); });
   return nq_check_launch(e);
 }
 

@@ -26,6 +26,18 @@ struct PrefillParams {
   int q_pos0;
   int B, Hq, Hkv, G, S, T, BM, nqb;
   float scale_log2;  // sm_scale * log2(e)
+  // fp32 kernel only (decode against a ragged or paged cache): sequence b
+  // holds kv_lens[b] + kv_extra keys, or none if that count lies outside
+  // [kv_extra, kv_max] (its rows then come out NaN; a sequence with no keys
+  // gives zeros); NULL = every sequence holds T.  With kv_lens and neither
+  // q_pos nor q_pos0 >= 0, a query sits at position keys - 1.
+  const int32_t* kv_lens;
+  int kv_extra, kv_max;
+  // paged K/V: key t of sequence b is row t % page of page
+  // bt[b * bts + t / page], strides (ksb, ksh, kss) = (page, head, row)
+  const int32_t* bt;
+  int64_t bts;
+  int page;
 };
 
 // The fp32 prefill (q, k, v, o all fp32; products on v_mfma_f32_32x32x2_f32).

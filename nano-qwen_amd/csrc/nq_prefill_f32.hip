@@ -18,6 +18,8 @@
 // 16-byte chunk: the 16 rows one ds_read_b128 of K serves, and the two rows
 // (k, k+4) one V^T read touches, land on distinct banks (D = 32: the V read
 // is 2-way).
+// The same kernel serves the fp32 decode (S = 1): per-sequence key counts and
+// a paged cache (block table) replace the uniform T and dense strides.
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
@@ -61,12 +63,22 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
   const int qblk = CAUSAL ? (p.nqb - 1 - qrank) : qrank;  // heaviest first
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
-  const int coff = p.T - p.S;
-  const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + coff) : p.T;
+  // keys of this sequence (-1: a length out of range, no keys and NaN rows)
+  int T = p.T;
+  if (p.kv_lens) {
+    const int l = p.kv_lens[b];
+    T = (l < 0 || l > p.kv_max - p.kv_extra) ? -1 : l + p.kv_extra;
+  }
+  const int coff = T - p.S;
+  const int kv_end = max(0, CAUSAL ? min(T, q0 + p.BM + coff) : T);
   const int ntiles = (kv_end + PF32_BN - 1) / PF32_BN;
 
-  const float* kbase = reinterpret_cast<const float*>(p.k) + b * p.ksb + kvh * p.ksh;
-  const float* vbase = reinterpret_cast<const float*>(p.v) + b * p.vsb + kvh * p.vsh;
+  // row `key` of this (batch, kv head): dense strides, or through the block table
+  auto krow = [&](const void* base, int64_t sb, int64_t sh, int64_t ss, int key) {
+    const float* f = reinterpret_cast<const float*>(base) + kvh * sh;
+    if (p.bt) return f + (int64_t)p.bt[b * p.bts + key / p.page] * sb + (int64_t)(key % p.page) * ss;
+    return f + b * sb + (int64_t)key * ss;
+  };
 
   // slot i = tid + 256u of a tile: row i / CPR, chunk i % CPR (coalesced rows)
   floatx4 kr[LPT], vr[LPT];
@@ -75,9 +87,9 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
     for (int u = 0; u < LPT; ++u) {
       const int i = tid + 64 * PF32_NW * u;
       const int key = tile * PF32_BN + i / CPR, c = i % CPR;
-      if (key < p.T) {
-        kr[u] = *reinterpret_cast<const floatx4*>(kbase + (int64_t)key * p.kss + c * 4);
-        vr[u] = *reinterpret_cast<const floatx4*>(vbase + (int64_t)key * p.vss + c * 4);
+      if (key < T) {
+        kr[u] = *reinterpret_cast<const floatx4*>(krow(p.k, p.ksb, p.ksh, p.kss, key) + c * 4);
+        vr[u] = *reinterpret_cast<const floatx4*>(krow(p.v, p.vsb, p.vsh, p.vss, key) + c * 4);
       } else {
         kr[u] = floatx4{};
         vr[u] = floatx4{};
@@ -93,7 +105,7 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
       vt[row * CPR + (c ^ Tl::vswz(row))] = vr[u];
     }
   };
-  fetch(0);
+  if (ntiles > 0) fetch(0);
 
   // this lane's query row: column r32 of this wave's 32 rows
   const int R = wave * 32 + r32;
@@ -128,7 +140,9 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
         }
       }
       if (p.cos_tab) {  // model/rope.py:133-161, rotate-half pairs (t, t + D/2)
-        const int pos = table_row(row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S), p.max_pos);
+        const bool from_len = p.kv_lens && !p.q_pos && p.q_pos0 < 0;  // decode: the newest key's position
+        const int pos = table_row(from_len ? T - 1 : row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S),
+                                  p.max_pos);
 #pragma unroll
         for (int t8 = 0; t8 < NT / 8; ++t8) {
           const floatx8 c = load_tab8(p.cos_tab, pos, D / 2, 8 * t8);
@@ -166,8 +180,8 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
 
     // keys past T, and (causal) keys past this row's frontier
     const int n0 = j * PF32_BN;
-    if (n0 + PF32_BN > p.T || (CAUSAL && n0 + PF32_BN - 1 > q0 + coff)) {
-      const int lim = CAUSAL ? min(p.T - 1, qi + coff) : p.T - 1;
+    if (n0 + PF32_BN > T || (CAUSAL && n0 + PF32_BN - 1 > q0 + coff)) {
+      const int lim = CAUSAL ? min(T - 1, qi + coff) : T - 1;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         if (n0 + (i / 4) * 8 + hh * 4 + (i % 4) > lim) s[i] = -INFINITY;
@@ -208,8 +222,18 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
 
   l_i = xor32_sum(l_i);
   if (!qvalid) return;
-  const float inv_l = 1.f / l_i;
   float* orow = reinterpret_cast<float*>(p.o) + b * p.osb + head * p.osh + (int64_t)qi * p.oss;
+  if (kv_end == 0) {  // no keys: zeros; a length out of range: NaN
+    const float f = T < 0 ? __builtin_nanf("") : 0.f;
+#pragma unroll
+    for (int dd = 0; dd < NDO; ++dd)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        *reinterpret_cast<floatx4*>(orow + dd * 32 + gq * 8 + hh * 4) = floatx4{f, f, f, f};
+    if (p.lse && hh == 0) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = -INFINITY;
+    return;
+  }
+  const float inv_l = 1.f / l_i;
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd)
 #pragma unroll

@@ -14,7 +14,7 @@ import nano_qwen_amd as nq
 from nano_qwen_amd import ops
 from oracle import (OracleKVCache, attention, attention_module_forward, attention_path, decode_path,
                     rms_norm, rope_tables, rotate_half)
-from tests.helpers import assert_bf16_close, randn, say
+from tests.helpers import assert_bf16_close, assert_close_for, assert_fp32_close, randn, say
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -51,8 +51,8 @@ def test_d32_row_kernel(dtype):
     qo, ko, _ = nq.qk_norm_rope(q=q.to(DEV), k=k.to(DEV), q_weight=qw.to(DEV), k_weight=kw.to(DEV), eps=1e-6,
                                 cos=cos.to(DEV), sin=sin.to(DEV), position_ids=pos.to(DEV))
     c, s = cos[pos][:, None], sin[pos][:, None]
-    assert_bf16_close(qo, rotate_half(rms_norm(q.float(), qw, 1e-6), c, s), "q-hat")
-    assert_bf16_close(ko, rotate_half(rms_norm(k.float(), kw, 1e-6), c, s), "k-hat")
+    assert_close_for(dtype, qo, rotate_half(rms_norm(q.float(), qw, 1e-6), c, s), "q-hat")
+    assert_close_for(dtype, ko, rotate_half(rms_norm(k.float(), kw, 1e-6), c, s), "k-hat")
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (8, 2), (16, 1)])
@@ -98,7 +98,7 @@ def test_d32_decode(dtype, chunk, Hq, Hkv):
     ref = decode_path(q.float(), kc.float(), vc.float(), lens, q_weight=qw, eps=1e-6, cos=cos, sin=sin,
                       q_pos=lens.long() - 1)
     assert torch.isfinite(o.float().cpu()).all()
-    assert_bf16_close(o, ref, "D=32 decode")
+    assert_close_for(dtype, o, ref, "D=32 decode")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -136,11 +136,14 @@ def test_d32_paged_fused_append(dtype):
         vdense[b, :, t] = vn[b]
     ref = decode_path(q.float(), kdense.float(), vdense.float(), lens + 1, q_weight=qw, eps=1e-6, cos=cos,
                       sin=sin, q_pos=lens.long())
-    assert_bf16_close(o, ref, "D=32 fused append")
+    assert_close_for(dtype, o, ref, "D=32 fused append")
     for b in range(B):
         t = int(lens[b])
         got = kp[int(bt[b, t // P]), :, t % P].float().cpu()
-        assert_bf16_close(got, kdense[b, :, t].float(), "appended K-hat row", max_abs=1e-2, mean_abs=2e-3)
+        if dtype == torch.float32:
+            assert_fp32_close(got, kdense[b, :, t], "appended K-hat row")
+        else:
+            assert_bf16_close(got, kdense[b, :, t].float(), "appended K-hat row", max_abs=1e-2, mean_abs=2e-3)
         assert torch.equal(vp[int(bt[b, t // P]), :, t % P].cpu(), vn[b])
 
 
@@ -222,14 +225,20 @@ def test_debug_yaml_attention_module(dtype):
     h = randn(2, 256, 256, seed=3281, dtype=dtype)
     out = attn(h.to(DEV))
     ref, _ = attention_module_forward(h, w, **kw)
-    assert_bf16_close(out, ref, "no cache", max_abs=3e-2)
+    if dtype == torch.float32:  # fp32 module: fp32 attention, fp32 gate
+        assert_fp32_close(out, ref, "no cache")
+    else:
+        assert_bf16_close(out, ref, "no cache", max_abs=3e-2)
     cache, ocache = nq.KVCache(), OracleKVCache()
     steps = [randn(1, 40, 256, seed=3282, dtype=dtype)] + [randn(1, 1, 256, seed=3283 + i, dtype=dtype)
                                                            for i in range(3)]
     for i, x in enumerate(steps):
         got = attn(x.to(DEV), kv_cache=cache)
         want, _ = attention_module_forward(x, w, kv_cache=ocache, **kw)
-        assert_bf16_close(got, want, f"cache step {i}", max_abs=3e-2)
+        if dtype == torch.float32:
+            assert_fp32_close(got, want, f"cache step {i}")
+        else:
+            assert_bf16_close(got, want, f"cache step {i}", max_abs=3e-2)
     assert cache.seq_len == ocache.seq_len == 43
 
 

@@ -5,7 +5,7 @@ import torch
 
 import nano_qwen_amd as nq
 from oracle import decode_path, rope_tables
-from tests.helpers import assert_bf16_close, randn, say
+from tests.helpers import assert_bf16_close, assert_close_for, randn, say
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -35,7 +35,7 @@ def test_decode_small_ragged(D, dtype, chunk):
     ref = decode_path(q.float(), kc.float(), vc.float(), lens, q_weight=qw, eps=1e-6, cos=cos,
                       sin=sin, q_pos=lens.long() - 1)
     assert torch.isfinite(o.float().cpu()).all()
-    assert_bf16_close(o, ref, "decode small")
+    assert_close_for(dtype, o, ref, "decode small")
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (8, 2), (64, 4), (32, 1)])

@@ -17,7 +17,7 @@ import torch
 import nano_qwen_amd as nq
 from nano_qwen_amd import ops
 from oracle import decode_path, rms_norm, rope_tables, rotate_half
-from tests.helpers import assert_bf16_close, randn, say
+from tests.helpers import assert_bf16_close, assert_close_for, randn, say
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -157,7 +157,7 @@ def test_fused_append_dense_layout(G, dtype):
     assert torch.equal(k2.nan_to_num(), k1.nan_to_num()) and torch.equal(v2.nan_to_num(), v1.nan_to_num())
     assert torch.equal(o2, o1), float((o2.float() - o1.float()).abs().max())
     ref = _oracle_append(q, kn, vn, kc, vc, lens, qw, kw, cos, sin, lens)
-    assert_bf16_close(o2, ref, "fused append vs oracle")
+    assert_close_for(dtype, o2, ref, "fused append vs oracle")
 
 
 @pytest.mark.parametrize("P", [32, 128])
