@@ -112,6 +112,11 @@ int nq_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, void* y,
  *   buffer to get o_proj's input layout directly).  q, k, v and o all use
  *   `dtype`; NQ_DTYPE_F32 runs every product in fp32 (v_mfma_f32_32x32x2_f32).
  * lse: optional fp32 (B, Hq, S) natural-log sum-exp of the scaled scores.
+ * key_lens: optional int32 (B): sequence b attends only keys
+ *   [0, key_lens[b]) -- the key-padding mask SDPA applies for a right-padded
+ *   batch (model/attention.py:110-114 with a (B, 1, 1, T) keep-mask, the
+ *   reward model's padding, training/reward_model.py:45).  0 gives zero rows,
+ *   a value outside [0, T] NaN rows (lse -inf).  NULL = all T keys.
  * q_weight: RMSNorm weight for Q (NULL = none); cos_tab/sin_tab: RoPE table
  *   for Q (NULL = none); q_pos / q_pos_base / q_pos0: Q positions as in
  *   nq_qk_norm_rope.
@@ -123,7 +128,8 @@ int nq_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, void* y,
  */
 int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                        void* o, const int64_t* o_strides, float* lse, int B, int Hq, int Hkv,
+                        void* o, const int64_t* o_strides, float* lse, const int32_t* key_lens,
+                        int B, int Hq, int Hkv,
                         int S, int T, int D, int dtype, const float* q_weight, float eps,
                         const float* cos_tab, const float* sin_tab, int max_pos,
                         const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
@@ -290,6 +296,8 @@ int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S);
  *   (B, Hq, S) from nq_attn_prefill_fwd (same q, k, v, causal and sm_scale).
  * dq (B, Hq, S, D), dk / dv (B, Hkv, T, D): outputs, fully written.
  * causal keeps key j for query i iff j <= i + T - S (needs S <= T).
+ * key_lens: optional int32 (B), as in nq_attn_prefill_fwd (the forward's
+ *   key padding): keys at or past key_lens[b] get zero dK / dV.
  * workspace: nq_attn_bwd_workspace_bytes(B, Hq, S) bytes.
  * Requires 128 % (Hq / Hkv) == 0.  Storage dtype bf16 (products on bf16
  * MFMA) or fp32 (products on fp32 MFMA, as the reference's fp32 autograd);
@@ -297,8 +305,9 @@ int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S);
  */
 int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
-                const void* dout, const int64_t* do_strides, const float* lse, void* dq,
-                const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                const void* dout, const int64_t* do_strides, const float* lse,
+                const int32_t* key_lens, void* dq, const int64_t* dq_strides, void* dk,
+                const int64_t* dk_strides, void* dv,
                 const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
                 int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream);
 

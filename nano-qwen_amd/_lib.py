@@ -51,7 +51,7 @@ SIGNATURES = {
     ]),
     "nq_attn_prefill_fwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,  # q, k, v, o (+ strides)
-        _p,                                          # lse
+        _p, _p,                                      # lse, key_lens
         _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype
         _p, _f32,                                    # q_weight, eps
         _p, _p, _i32,                                # cos, sin, max_pos
@@ -113,7 +113,7 @@ SIGNATURES = {
     "nq_attn_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "nq_attn_bwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p,             # q, k, v (+ strides)
-        _p, _i64p, _p, _i64p, _p,                    # o, dout (+ strides), lse
+        _p, _i64p, _p, _i64p, _p, _p,                # o, dout (+ strides), lse, key_lens
         _p, _i64p, _p, _i64p, _p, _i64p,             # dq, dk, dv (+ strides)
         _p, _i64,                                    # workspace, workspace_bytes
         _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype

@@ -16,9 +16,14 @@ Dispatch (following kernels/flash_attn.py:139's convention):
   * autograd (training, no cache) -> the same kernels through an autograd
     Function whose backward is the FlashAttention-2 backward kernels plus the
     QK-Norm + RoPE backward kernel (nano_qwen_amd.autograd);
-  * an explicit attention_mask, attention dropout, or autograd with a cache
-    -> torch ops on the device, the reference's own arithmetic (SDPA), since
-    the kernels are maskless;
+  * an attention_mask that is a key-padding mask (keeps, for every head and
+    query, the same prefix [0, L_b) of each sequence's keys: a bool or 0/-inf
+    float mask of shape (B or 1, 1, 1, T), (1, T) or (T,), as a right-padded
+    batch gives) and no cache -> the same kernels with per-sequence key
+    counts, non-causal as SDPA is with a mask (attention.py:113), forward and
+    backward;
+  * any other attention_mask, attention dropout, or autograd with a cache
+    -> torch ops on the device, the reference's own arithmetic (SDPA);
   * host tensors -> RuntimeError (the kernels are the product; there is no
     CPU path).
 
@@ -47,6 +52,49 @@ from .rope import RotaryEmbedding
 
 # Counters of which path forward() took (kernel launches vs torch fallback).
 stats = {"kernel_forward": 0, "kernel_train_forward": 0, "torch_forward": 0}
+
+
+def key_padding_lengths(mask: torch.Tensor, B: int, T: int) -> Optional[torch.Tensor]:
+    """Per-sequence key counts (int32 (B,), on the mask's device) when ``mask``,
+    broadcast as SDPA broadcasts attn_mask against (B, H, S, T), keeps for
+    every head and query the same prefix [0, L_b) of sequence b's keys with
+    L_b >= 1 (a right-padded batch); None for any other mask (a query-dependent
+    or head-dependent pattern, holes, an all-padding row, a float mask with
+    values other than 0 and -inf, or a dtype SDPA refuses), which then takes
+    SDPA itself.  The answer is cached on the mask tensor (keyed by its
+    version), so a model that hands one mask to every layer pays one host sync.
+    """
+    if mask.dim() > 4 or mask.dim() == 0:
+        return None
+    cached = getattr(mask, "_nq_key_lens", None)
+    if cached is not None and cached[0] == mask._version and cached[1] == (B, T):
+        return cached[2]
+    lens = _prefix_lengths(mask, B, T)
+    try:
+        mask._nq_key_lens = (mask._version, (B, T), lens)
+    except (AttributeError, RuntimeError):
+        pass
+    return lens
+
+
+def _prefix_lengths(mask: torch.Tensor, B: int, T: int) -> Optional[torch.Tensor]:
+    m = mask.reshape((1,) * (4 - mask.dim()) + tuple(mask.shape))  # SDPA's broadcast alignment
+    if m.shape[1] != 1 or m.shape[2] != 1 or m.shape[3] != T or m.shape[0] not in (1, B):
+        return None
+    m = m[:, 0, 0]
+    if m.dtype == torch.bool:
+        keep = m
+    elif m.is_floating_point():
+        keep = m == 0
+        if not bool((keep | (m == float("-inf"))).all()):
+            return None  # an additive bias, not a keep / drop mask
+    else:
+        return None  # SDPA raises for other dtypes; let it
+    lens = keep.sum(-1, dtype=torch.int32)
+    prefix = torch.arange(T, device=m.device)[None, :] < lens[:, None]
+    if not bool(((keep == prefix).all() & (lens >= 1).all()).item()):
+        return None
+    return lens.expand(B).contiguous()
 
 
 class KVCache:
@@ -370,9 +418,13 @@ class Attention(nn.Module):
         kw = self.k_norm.weight if self.qk_norm else None
         needs_grad = torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (q, k, v, qw, kw))
-        if attention_mask is not None or dropout or (needs_grad and kv_cache is not None):
+        key_lens = None
+        if attention_mask is not None and kv_cache is None and not dropout:
+            key_lens = key_padding_lengths(attention_mask, B, S)
+        if (attention_mask is not None and key_lens is None) or dropout or (needs_grad and kv_cache is not None):
             stats["torch_forward"] += 1
             return self._torch_forward(q, k, v, position_ids, attention_mask, kv_cache)
+        causal = key_lens is None  # SDPA is not causal once a mask is given
 
         q4 = q.view(B, S, H, D).transpose(1, 2)
         k4 = k.view(B, S, Hkv, D).transpose(1, 2)
@@ -384,7 +436,8 @@ class Attention(nn.Module):
             # no cache: attention.py:113 with kv_cache None)
             stats["kernel_train_forward"] += 1
             o = autograd.attention_core(q4, k4, v4, qw, kw, cos=cos, sin=sin,
-                                        position_ids=position_ids, eps=eps, causal=True)
+                                        position_ids=position_ids, eps=eps, causal=causal,
+                                        key_lens=key_lens)
             return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
         stats["kernel_forward"] += 1
         if isinstance(kv_cache, PagedKVCache):
@@ -397,7 +450,8 @@ class Attention(nn.Module):
             ops.qk_norm_rope(k=k4, k_out=k_hat, k_weight=kw, eps=eps, cos=cos, sin=sin,
                              position_ids=position_ids, pos_offset=pos_offset)
             o = ops.attention_prefill(q4, k_hat, v4, q_weight=qw, eps=eps, cos=cos, sin=sin,
-                                      position_ids=position_ids, pos_offset=pos_offset, causal=True)
+                                      position_ids=position_ids, pos_offset=pos_offset, causal=causal,
+                                      key_lens=key_lens)
             return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
 
         if kv_cache.lens is not None:

@@ -117,18 +117,21 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
   const int qblk = CAUSAL ? (p.nqb - 1 - qrank) : qrank;
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
-  const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + p.coff) : p.T;
+  const int Tk = bw_keys(p, b);  // keys this sequence attends
+  const int kv_end = CAUSAL ? min(Tk, q0 + p.BM + p.coff) : Tk;
   const int ntiles = (kv_end + BW_BN - 1) / BW_BN;
 
   const T* kb0 = reinterpret_cast<const T*>(p.k) + b * p.ksb + kvh * p.ksh;
   const T* vb0 = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
   auto stage = [&](int j, int buf) {
     const int n0 = j * BW_BN;
-    bw_tile<D, T, BW_BN, true, NW>(smem + buf * 2 * TB, kb0 + (int64_t)n0 * p.kss, p.kss, p.T - n0, wave, lane);
-    bw_tile<D, T, BW_BN, false, NW>(smem + buf * 2 * TB + TB, vb0 + (int64_t)n0 * p.vss, p.vss, p.T - n0, wave,
+    // rows past the sequence's keys clamp to its last key (masked; padding
+    // rows are never read)
+    bw_tile<D, T, BW_BN, true, NW>(smem + buf * 2 * TB, kb0 + (int64_t)n0 * p.kss, p.kss, Tk - n0, wave, lane);
+    bw_tile<D, T, BW_BN, false, NW>(smem + buf * 2 * TB + TB, vb0 + (int64_t)n0 * p.vss, p.vss, Tk - n0, wave,
                                     lane);
   };
-  stage(0, 0);  // its latency overlaps the Q / dO loads below
+  if (ntiles > 0) stage(0, 0);  // its latency overlaps the Q / dO loads below
 
   const int R = wave * 32 + r32;
   const int g = R / p.BM, pr = R - g * p.BM;
@@ -202,7 +205,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) dqacc[dd] = floatx16{};
   // last key this row sees (rows past S see none)
-  const int lim = !qvalid ? -1 : (CAUSAL ? min(qi + p.coff, p.T - 1) : p.T - 1);
+  const int lim = !qvalid ? -1 : (CAUSAL ? min(qi + p.coff, Tk - 1) : Tk - 1);
 
   for (int j = 0; j < ntiles; ++j) {
     const int n0 = j * BW_BN;
@@ -215,7 +218,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
     const uint32_t ka = lds_addr(Kt);  // the V tile is TB bytes on
     // a tile inside every row's bounds (all keys below T and at or before
     // the block's first query's frontier, no rows past S) skips the mask
-    const bool full = n0 + BW_BN <= p.T && q0 + p.BM <= p.S && (!CAUSAL || n0 + BW_BN - 1 <= q0 + p.coff);
+    const bool full = n0 + BW_BN <= Tk && q0 + p.BM <= p.S && (!CAUSAL || n0 + BW_BN - 1 <= q0 + p.coff);
     // the two 32-key blocks of the tile (kb a compile-time constant, so its
     // LDS offset goes into the read instructions)
     auto key_block = [&](auto KB) {
@@ -313,12 +316,13 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int k0 = kblk * BW_KEYS;
   const int key = k0 + wave * 32 + r32;  // this lane's key (C column)
-  const int key_c = key < p.T ? key : p.T - 1;
+  const int Tk = bw_keys(p, b);  // keys past Tk are padding: zero gradients, rows never read
+  const int key_c = key < Tk ? key : k0;  // a padded key's K row: the block's first (read only if < Tk)
 
   // the work list: (head g, query tile qt) for queries that see a key of this
-  // block (q + coff >= k0)
+  // block (q + coff >= k0); none when the whole block is padding
   const int qstart = CAUSAL ? max(0, k0 - p.coff) / BW_BQ * BW_BQ : 0;
-  const int nqt = qstart < p.S ? (p.S - qstart + BW_BQ - 1) / BW_BQ : 0;
+  const int nqt = (qstart < p.S && k0 < Tk) ? (p.S - qstart + BW_BQ - 1) / BW_BQ : 0;
   const int niter = p.G * nqt;
   // bf16 Q / dO tiles: this wave's DMA instruction i fills LDS bytes
   // [(wave + 4i) * 1024, +1024), the lane's 16 bytes lying in tile row
@@ -370,7 +374,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   // without work issues none, so none is left in flight at exit).
   if (niter > 0) {
     bw_tile<D, T, BW_KEYS, false>(Vs, reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh + (int64_t)k0 * p.vss,
-                                  p.vss, p.T - k0, wave, lane);
+                                  p.vss, Tk - k0, wave, lane);
     stage(gn, qtn, 0);
     advance(gn, qtn);
   }
@@ -422,7 +426,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
     // a wave whose keys all lie past T, or (causal) after every query of the
     // step, has P = 0 there: nothing to add
     const int kw0 = k0 + wave * 32;
-    if (kw0 >= p.T || (CAUSAL && kw0 > qt + BW_BQ - 1 + p.coff)) continue;
+    if (kw0 >= Tk || (CAUSAL && kw0 > qt + BW_BQ - 1 + p.coff)) continue;
     const unsigned char* Qt = smem + (it & 1) * BUF;
     const unsigned char* Dt = Qt + TB;
     const float* lse_t = reinterpret_cast<const float*>(Qt + 2 * TB);
@@ -475,7 +479,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
             if constexpr (decltype(masked)::value) {
               // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
               const int q = qt + r0 + u;
-              const bool keep = key < p.T && q < p.S && (!CAUSAL || key <= q + p.coff);
+              const bool keep = key < Tk && q < p.S && (!CAUSAL || key <= q + p.coff);
               x = keep ? x : -INFINITY;
             }
             const float pe = fast_exp2(x);
@@ -488,7 +492,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
       }
     };
     const int kw1 = kw0 + 31;  // the wave's last key
-    if (kw1 < p.T && qt + BW_BQ <= p.S && (!CAUSAL || kw1 <= qt + p.coff))
+    if (kw1 < Tk && qt + BW_BQ <= p.S && (!CAUSAL || kw1 <= qt + p.coff))
       probs(std::false_type{});
     else
       probs(std::true_type{});
@@ -655,7 +659,8 @@ extern "C" int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S) {
 
 extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                            const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
-                           const void* dout, const int64_t* do_strides, const float* lse, void* dq,
+                           const void* dout, const int64_t* do_strides, const float* lse,
+                           const int32_t* key_lens, void* dq,
                            const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
                            const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
                            int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream) {
@@ -700,6 +705,7 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   p.dksb = dk_strides[0]; p.dksh = dk_strides[1]; p.dkss = dk_strides[2];
   p.dvsb = dv_strides[0]; p.dvsh = dv_strides[1]; p.dvss = dv_strides[2];
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
+  p.kv_lens = key_lens;
   // dQ workgroups: 8 waves (256 query rows: each K/V tile load serves twice
   // the rows) when that still gives enough workgroups to fill the device
   const int64_t wide_wgs = (int64_t)B * Hkv * ((S + 256 / G - 1) / (256 / G));

@@ -26,7 +26,17 @@ struct BwdParams {
   int64_t dqsb, dqsh, dqss, dksb, dksh, dkss, dvsb, dvsh, dvss;
   int B, Hq, Hkv, G, S, T, BM, nqb, coff;
   float scale, scale_log2;
+  // key padding: sequence b attends keys [0, kv_lens[b]) (clamped to
+  // [0, T]; the rest get zero gradients); NULL = all T keys
+  const int32_t* kv_lens;
 };
+
+// Keys sequence b attends.
+__device__ __forceinline__ int bw_keys(const BwdParams& p, int b) {
+  if (!p.kv_lens) return p.T;
+  const int l = p.kv_lens[b];
+  return l < 0 ? 0 : (l > p.T ? p.T : l);
+}
 
 // Scratch slot of query row s of (batch b, head h): LSE * log2(e) at the
 // returned index, Delta 32 floats later.

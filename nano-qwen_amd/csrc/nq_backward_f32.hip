@@ -87,13 +87,14 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
   const int qblk = CAUSAL ? (p.nqb - 1 - qrank) : qrank;
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
-  const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + p.coff) : p.T;
+  const int Tk = bw_keys(p, b);  // keys this sequence attends
+  const int kv_end = CAUSAL ? min(Tk, q0 + p.BM + p.coff) : Tk;
   const int ntiles = (kv_end + BF32_TILE - 1) / BF32_TILE;
   const float* kbase = reinterpret_cast<const float*>(p.k) + b * p.ksb + kvh * p.ksh;
   const float* vbase = reinterpret_cast<const float*>(p.v) + b * p.vsb + kvh * p.vsh;
-  TileCopy<D> kc, vc;
-  kc.fetch(kbase, p.kss, 0, p.T);
-  vc.fetch(vbase, p.vss, 0, p.T);
+  TileCopy<D> kc, vc;  // rows past the sequence's keys read as zeros (padding is never read)
+  kc.fetch(kbase, p.kss, 0, Tk);
+  vc.fetch(vbase, p.vss, 0, Tk);
 
   const int R = wave * 32 + r32;
   const int g = R / p.BM, pr = R - g * p.BM;
@@ -151,8 +152,8 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
     vc.stash(vt);
     __syncthreads();
     if (j + 1 < ntiles) {
-      kc.fetch(kbase, p.kss, (j + 1) * BF32_TILE, p.T);
-      vc.fetch(vbase, p.vss, (j + 1) * BF32_TILE, p.T);
+      kc.fetch(kbase, p.kss, (j + 1) * BF32_TILE, Tk);
+      vc.fetch(vbase, p.vss, (j + 1) * BF32_TILE, Tk);
     }
     // S^T = K Q^T and dP^T = V dO^T (MFMA row = key r32 of the tile)
     floatx16 s = floatx16{}, dp = floatx16{};
@@ -167,7 +168,7 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
       }
     }
     const int n0 = j * BF32_TILE;
-    const int lim = CAUSAL ? min(p.T - 1, qi + p.coff) : p.T - 1;
+    const int lim = CAUSAL ? min(Tk - 1, qi + p.coff) : Tk - 1;
     float ds[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -214,11 +215,13 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dkdv_f32_kernel(BwdParams p)
   const int k0 = kblk * KEYS;
   const int key = k0 + wave * 32 + r32;  // this lane's key column
   const bool kvalid = key < p.T;
+  const bool kattend = key < bw_keys(p, b);  // keys past the sequence's count: zero gradients
 
-  // this lane's halves of its K and V rows (B operands of S and dP)
+  // this lane's halves of its K and V rows (B operands of S and dP); zeros for
+  // keys past T or the sequence's count (padding rows are never read)
   float kr[NT], vr[NT];
   {
-    const int kc = kvalid ? key : p.T - 1;
+    const int kc = kattend ? key : 0;
     const float* krow = reinterpret_cast<const float*>(p.k) + b * p.ksb + kvh * p.ksh + (int64_t)kc * p.kss + hh * NT;
     const float* vrow = reinterpret_cast<const float*>(p.v) + b * p.vsb + kvh * p.vsh + (int64_t)kc * p.vss + hh * NT;
 #pragma unroll
@@ -227,8 +230,8 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dkdv_f32_kernel(BwdParams p)
       const floatx4 c = *reinterpret_cast<const floatx4*>(vrow + 4 * t4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        kr[4 * t4 + e] = a[e];
-        vr[4 * t4 + e] = c[e];
+        kr[4 * t4 + e] = kattend ? a[e] : 0.f;
+        vr[4 * t4 + e] = kattend ? c[e] : 0.f;
       }
     }
   }
@@ -273,7 +276,7 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dkdv_f32_kernel(BwdParams p)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ql = (i / 4) * 8 + hh * 4 + (i % 4);
-        const bool keep = kvalid && (!CAUSAL || key <= s0 + ql + p.coff);
+        const bool keep = kattend && (!CAUSAL || key <= s0 + ql + p.coff);
         pe[i] = keep ? fast_exp2(s[i] * p.scale_log2 - lse2s[ql]) : 0.f;
         ds[i] = pe[i] * (dp[i] - dlts[ql]);
       }

@@ -139,8 +139,21 @@ prefill_kernel(PrefillParams p) {
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
   const int coff = p.T - p.S;
+  // keys of this sequence (key padding: fewer than T)
+  const int Tk = pf_keys(p, b);
+  if (Tk <= 0) {  // no keys: zeros; a length out of range: NaN
+    const float f = Tk < 0 ? __builtin_nanf("") : 0.f;
+    for (int r = threadIdx.x; r < 32 * NW; r += 64 * NW) {
+      const int g = r / p.BM, qi = q0 + r - g * p.BM;
+      if (qi >= p.S) continue;
+      T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (kvh * p.G + g) * p.osh + (int64_t)qi * p.oss;
+      for (int d = 0; d < D; ++d) orow[d] = (T)f;
+      if (p.lse) p.lse[((int64_t)b * p.Hq + kvh * p.G + g) * p.S + qi] = -INFINITY;
+    }
+    return;
+  }
 
-  const int kv_end = CAUSAL ? min(p.T, q0 + p.BM + coff) : p.T;
+  const int kv_end = CAUSAL ? min(Tk, q0 + p.BM + coff) : Tk;
   const int ntiles = (kv_end + PF_BN - 1) / PF_BN;
   // K/V are bf16 in memory: they go to LDS unconverted
   const unsigned char* kbase =
@@ -164,7 +177,7 @@ prefill_kernel(PrefillParams p) {
   auto load_tile = [&](const unsigned char* base, int64_t row_bytes, uint32_t off, int lds_off,
                        int tile) {
     const int lds_w = lds_off + wave * 1024;
-    if (tile * PF_BN + PF_BN <= p.T) {
+    if (tile * PF_BN + PF_BN <= Tk) {
       if constexpr (NW == 4) {
         // buffer loads: the tile's base in a scalar descriptor, the lane offset
         // in one 32-bit VGPR, the instruction's row step as a scalar offset.
@@ -187,7 +200,7 @@ prefill_kernel(PrefillParams p) {
       const uint32_t chunk_off = off - (uint32_t)(row0 * row_bytes);
 #pragma unroll
       for (int m = 0; m < Tl::LOADS; ++m) {
-        const int key = min(tile * PF_BN + row0 + m * NW * RPI, p.T - 1);
+        const int key = min(tile * PF_BN + row0 + m * NW * RPI, Tk - 1);
         global_load_lds16(base + key * row_bytes + chunk_off, smem + lds_w + m * NW * 1024);
       }
     }
@@ -322,8 +335,8 @@ prefill_kernel(PrefillParams p) {
 
   // masking of tile n0: keys past T, and (causal) keys past this row's frontier
   auto mask_tile = [&](floatx16* s, int n0) {
-    if ((n0 + PF_BN > p.T) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff)) {
-      const int lim = CAUSAL ? min(p.T - 1, qi + coff) : p.T - 1;
+    if ((n0 + PF_BN > Tk) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff)) {
+      const int lim = CAUSAL ? min(Tk - 1, qi + coff) : Tk - 1;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -474,7 +487,7 @@ prefill_kernel(PrefillParams p) {
   // step whose next tile is one of them carries no mask branch.  That branch would
   // split the step into basic blocks, and the compiler would then sink the exp2
   // work of P[j] below the S[j+1] MFMAs it is meant to interleave with.
-  const int jfree = min(ntiles, min(p.T / PF_BN, CAUSAL ? (q0 + coff + 1) / PF_BN : ntiles));
+  const int jfree = min(ntiles, min(Tk / PF_BN, CAUSAL ? (q0 + coff + 1) / PF_BN : ntiles));
   int j = 0;
   for (; j + 2 < jfree; j += 2) {
     step(I0{}, Yes{}, No{}, j);
@@ -537,7 +550,8 @@ using namespace nq;
 extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                                    const int64_t* k_strides, const void* v,
                                    const int64_t* v_strides, void* o, const int64_t* o_strides,
-                                   float* lse, int B, int Hq, int Hkv, int S, int T, int D,
+                                   float* lse, const int32_t* key_lens, int B, int Hq, int Hkv, int S,
+                                   int T, int D,
                                    int dtype, const float* q_weight, float eps,
                                    const float* cos_tab, const float* sin_tab, int max_pos,
                                    const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
@@ -577,6 +591,7 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   p.qw = q_weight; p.eps = eps; p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
   p.q_pos = q_pos; p.q_pos_base = q_pos_base; p.q_pos0 = q_pos0;
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
+  p.kv_lens = key_lens; p.kv_extra = 0; p.kv_max = T;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
   const bool fuse = q_weight != nullptr || cos_tab != nullptr;

@@ -26,19 +26,27 @@ struct PrefillParams {
   int q_pos0;
   int B, Hq, Hkv, G, S, T, BM, nqb;
   float scale_log2;  // sm_scale * log2(e)
-  // fp32 kernel only (decode against a ragged or paged cache): sequence b
-  // holds kv_lens[b] + kv_extra keys, or none if that count lies outside
-  // [kv_extra, kv_max] (its rows then come out NaN; a sequence with no keys
-  // gives zeros); NULL = every sequence holds T.  With kv_lens and neither
-  // q_pos nor q_pos0 >= 0, a query sits at position keys - 1.
+  // Per-sequence key counts (key padding, ragged or paged caches): sequence
+  // b holds keys [0, kv_lens[b] + kv_extra), or none if kv_lens[b] lies
+  // outside [0, kv_max - kv_extra] (its rows then come out NaN; a sequence
+  // with no keys gives zeros); NULL = every sequence holds T.  With kv_lens
+  // and neither q_pos nor q_pos0 >= 0 (decode), a query sits at position
+  // keys - 1.
   const int32_t* kv_lens;
   int kv_extra, kv_max;
-  // paged K/V: key t of sequence b is row t % page of page
+  // paged K/V (fp32 kernel): key t of sequence b is row t % page of page
   // bt[b * bts + t / page], strides (ksb, ksh, kss) = (page, head, row)
   const int32_t* bt;
   int64_t bts;
   int page;
 };
+
+// Keys of sequence b (-1: a length out of range).
+__device__ __forceinline__ int pf_keys(const PrefillParams& p, int b) {
+  if (!p.kv_lens) return p.T;
+  const int l = p.kv_lens[b];
+  return (l < 0 || l > p.kv_max - p.kv_extra) ? -1 : l + p.kv_extra;
+}
 
 // The fp32 prefill (q, k, v, o all fp32; products on v_mfma_f32_32x32x2_f32).
 // p.BM must be 128 / G (4 waves of 32 query rows).

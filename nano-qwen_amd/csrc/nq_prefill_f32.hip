@@ -64,11 +64,7 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
   // keys of this sequence (-1: a length out of range, no keys and NaN rows)
-  int T = p.T;
-  if (p.kv_lens) {
-    const int l = p.kv_lens[b];
-    T = (l < 0 || l > p.kv_max - p.kv_extra) ? -1 : l + p.kv_extra;
-  }
+  const int T = pf_keys(p, b);
   const int coff = T - p.S;
   const int kv_end = max(0, CAUSAL ? min(T, q0 + p.BM + coff) : T);
   const int ntiles = (kv_end + PF32_BN - 1) / PF32_BN;

@@ -97,6 +97,16 @@ def _i32(t: Optional[torch.Tensor], device) -> Optional[torch.Tensor]:
     return t
 
 
+def _key_lens(key_lens: Optional[torch.Tensor], B: int, device) -> Optional[torch.Tensor]:
+    """int32 (B,) per-sequence key counts on the device, or None."""
+    if key_lens is None:
+        return None
+    kl = _i32(key_lens.reshape(-1), device)
+    if kl.numel() != B:
+        raise ValueError(f"key_lens must hold one count per sequence ({B}), got {kl.numel()}")
+    return kl
+
+
 def _tables(cos, sin, device):
     if cos is None:
         return None, None, 0
@@ -261,6 +271,7 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                       position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
                       pos_base: Optional[torch.Tensor] = None,
                       causal: bool = True, sm_scale: Optional[float] = None,
+                      key_lens: Optional[torch.Tensor] = None,
                       out: Optional[torch.Tensor] = None, return_lse: bool = False,
                       plan: bool = False):
     """GQA prefill attention with QK-Norm + RoPE of Q fused into its load.
@@ -268,7 +279,8 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     q: (B, Hq, S, D) pre-norm queries (norm/rope skipped when q_weight / cos
     are None); k: (B, Hkv, T, D) keys as stored (already normed and rotated);
     v: (B, Hkv, T, D).  ``causal`` keeps key j for query i iff j <= i + T - S.
-    Returns o shaped (B, Hq, S, D); by default it is a transposed view of a
+    ``key_lens`` (int, (B,)) limits sequence b to keys [0, key_lens[b]): key
+    padding.  Returns o shaped (B, Hq, S, D); by default it is a transposed view of a
     contiguous (B, S, Hq, D) buffer, so ``o.transpose(1, 2).reshape(B, S, -1)``
     (o_proj's input, model/attention.py:117) costs nothing.  With
     ``return_lse`` also returns the fp32 (B, Hq, S) log-sum-exp.  With
@@ -290,6 +302,7 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     _rows_out(out, "out")
     lse = torch.empty(B, Hq, S, dtype=torch.float32, device=q.device) if return_lse else None
     dev = q.device
+    kl = _key_lens(key_lens, B, dev)
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
     pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
     pb = _i32(pos_base, dev)
@@ -297,12 +310,12 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     st = _lib.strides3
     args = (
         _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
-        _ptr(out), st(out.stride()[:3]), _ptr(lse),
+        _ptr(out), st(out.stride()[:3]), _ptr(lse), _ptr(kl),
         B, Hq, Hkv, S, T, D, dt, _ptr(qw), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
         _ptr(pos), _ptr(pb), int(pos_offset), int(bool(causal)),
         float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
     call = KernelCall(_lib.load().nq_attn_prefill_fwd, args, len(args) - 1, "nq_attn_prefill_fwd",
-                      (q, k, v, cos_t, sin_t, pos, pb, qw), (out, lse) if return_lse else out)
+                      (q, k, v, cos_t, sin_t, pos, pb, qw, kl), (out, lse) if return_lse else out)
     return call if plan else call.launch()
 
 
@@ -585,15 +598,16 @@ def attention_merge_(o: torch.Tensor, lse: torch.Tensor, o_part: torch.Tensor,
 
 def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                        dout: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
-                       sm_scale: Optional[float] = None,
+                       sm_scale: Optional[float] = None, key_lens: Optional[torch.Tensor] = None,
                        workspace: Optional[torch.Tensor] = None, plan: bool = False):
     """FlashAttention-2 backward: (dq, dk, dv) of o = softmax(scale q k^T) v.
 
     q: (B, Hq, S, D), k/v: (B, Hkv, T, D) as the forward attended them (after
     QK-Norm and RoPE); o, dout: (B, Hq, S, D); lse: the forward's fp32
     (B, Hq, S) log-sum-exp (``attention_prefill(..., return_lse=True)`` with
-    the same causal and sm_scale).  dk/dv sum the gradients of the G query
-    heads that share a kv head.  Returns fresh (dq, dk, dv) in q's dtype.
+    the same causal, sm_scale and key_lens).  dk/dv sum the gradients of the
+    G query heads that share a kv head; keys past key_lens[b] get zeros.
+    Returns fresh (dq, dk, dv) in q's dtype.
     """
     _require_device(q, k, v, o, dout, lse)
     B, Hq, S, D = q.shape
@@ -610,6 +624,7 @@ def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: tor
     q, k, v, o, dout = (_rows_in(t) for t in (q, k, v, o, dout))
     lse = lse.contiguous()
     dev = q.device
+    kl = _key_lens(key_lens, B, dev)
     dq = torch.empty(B, S, Hq, D, dtype=q.dtype, device=dev).transpose(1, 2)
     dk = torch.empty(B, T, Hkv, D, dtype=q.dtype, device=dev).transpose(1, 2)
     dv = torch.empty(B, T, Hkv, D, dtype=q.dtype, device=dev).transpose(1, 2)
@@ -620,13 +635,13 @@ def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: tor
     st = _lib.strides3
     args = (
         _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
-        _ptr(o), st(o.stride()[:3]), _ptr(dout), st(dout.stride()[:3]), _ptr(lse),
+        _ptr(o), st(o.stride()[:3]), _ptr(dout), st(dout.stride()[:3]), _ptr(lse), _ptr(kl),
         _ptr(dq), st(dq.stride()[:3]), _ptr(dk), st(dk.stride()[:3]), _ptr(dv), st(dv.stride()[:3]),
         _ptr(workspace), workspace.numel() * workspace.element_size(),
         B, Hq, Hkv, S, T, D, _code(q), int(bool(causal)),
         float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
     call = KernelCall(lib.nq_attn_bwd, args, len(args) - 1, "nq_attn_bwd",
-                      (q, k, v, o, dout, lse, workspace), (dq, dk, dv))
+                      (q, k, v, o, dout, lse, workspace, kl), (dq, dk, dv))
     return call if plan else call.launch()
 
 

@@ -43,15 +43,15 @@ def test_argument_errors_need_no_gpu():
     """Validation happens before any HIP call, so it is testable on the CPU."""
     lib = _lib.load()
     st = _lib.strides3((0, 0, 0))
-    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None,
+    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None, None,
                                  1, 8, 2, 4, 4, 96, 0, None, 1e-6, None, None, 0,
                                  None, None, 0, 1, 0.0, None)
     assert rc == _lib.NQ_ERR_UNSUPPORTED and b"head_dim" in lib.nq_last_error()
-    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None,
+    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None, None,
                                  1, 8, 3, 4, 4, 128, 0, None, 1e-6, None, None, 0,
                                  None, None, 0, 1, 0.0, None)
     assert rc == _lib.NQ_ERR_INVALID and b"divisible" in lib.nq_last_error()
-    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None,
+    rc = lib.nq_attn_prefill_fwd(None, st, None, st, None, st, None, st, None, None,
                                  1, 8, 2, 8, 4, 128, 0, None, 1e-6, None, None, 0,
                                  None, None, 0, 1, 0.0, None)
     assert rc == _lib.NQ_ERR_INVALID and b"S <= T" in lib.nq_last_error()
