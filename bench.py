@@ -16,8 +16,14 @@ prefill kernel's own FLOPs by its average duration from HIP events recorded
 on its launch stream.  ``secondary`` holds the other workloads, each with its
 roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs
 2.5x the forward's, the five matrix products of FlashAttention-2).
-``cpu_baseline`` times the oracle (fp32 torch on the host cores) on a bounded
-sample.
+``cpu_baseline`` (top level for the headline, inside each ``secondary`` entry
+for the others) times the reference's own composition -- QK-Norm, RoPE,
+repeat_interleave, SDPA, restated in the oracle -- in fp32 on the host cores, on
+each workload's own inputs: C2/C3 and the C2 backward in full, the decode as
+B=1 slices with their own lengths, C5 as one KV group of four and the C3
+backward as one batch row of four (extrapolations stated in ``sample``).
+``cores`` is the number of threads torch used; ``host_cpu_count`` is
+os.cpu_count().  ``roofline.traffic`` is profile-derived (``traffic_source``).
 """
 
 from __future__ import annotations
@@ -284,38 +290,143 @@ def time_workload(w, steps, warmup):
     return wall_ms / steps, avg_kernel, kernel_ms[len(kernel_ms) // 2]
 
 
-def cpu_baseline(budget_s=10.0):
-    """The oracle (fp32 torch on the host) on the same Qwen3-1.7B-like prefill shape.
+def _host():
+    """Host threads used by torch's CPU kernels and the machine's CPU counts."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"cores": torch.get_num_threads(), "host_cpu_count": os.cpu_count(),
+            "affinity_cpus": affinity}
 
-    Sample: batch rows of B8 S2048 Hq16 Hkv8 D128 (one row = all 16 heads of one
-    sequence), run row after row -- cycling over the batch -- until ~budget_s of
-    CPU time is spent; FLOPs counted as on the GPU.
-    """
-    from oracle import attention_path
-    threads = torch.get_num_threads()
-    B, S, Hq, Hkv, D = 8, 2048, 16, 8, 128
-    g = torch.Generator().manual_seed(1001)
-    q = torch.randn(1, Hq, S, D, generator=g)
-    k = torch.randn(1, Hkv, S, D, generator=g)
-    v = torch.randn(1, Hkv, S, D, generator=g)
-    w = 1 + 0.02 * torch.randn(D, generator=g)
-    from nano_qwen_amd.rope import build_tables
-    cos, sin = build_tables(D, S, 1e6)
+
+def _cpu(t):
+    return t.detach().float().cpu().contiguous()
+
+
+def cpu_prefill(w, groups=None):
+    """The reference's prefill composition (QK-Norm, RoPE, repeat_interleave, SDPA;
+    model/attention.py:95-115) in fp32 on the host cores, on the workload's own
+    inputs, one batch row at a time.  ``groups``: time only the first KV groups
+    (each Hq/Hkv query heads with their KV head) and extrapolate."""
+    from oracle import reference_path_sdpa
+    B, S, Hq, Hkv, D = w.B, w.S, w.Hq, w.Hkv, w.D
+    G = Hq // Hkv
+    ng = Hkv if groups is None else groups
+    cos, sin, qw, kw = _cpu(w.cos)[:S], _cpu(w.sin)[:S], _cpu(w.qw), _cpu(w.kw)
     pos = torch.arange(S)
-    rows, t0 = 0, time.perf_counter()
-    while True:
-        attention_path(q, k, v, q_weight=w, k_weight=w, eps=1e-6, cos=cos, sin=sin, q_pos=pos,
-                       causal=True)
-        rows += 1
-        if time.perf_counter() - t0 > budget_s:
+    sw = min(S, 8192)                         # warm-up, untimed: row 0's first 8192 positions
+    reference_path_sdpa(_cpu(w.q[:1, :ng * G, :sw]), _cpu(w.k[:1, :ng, :sw]), _cpu(w.v[:1, :ng, :sw]),
+                        q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin, q_pos=pos[:sw])
+    dt = 0.0
+    for b in range(B):
+        q, k, v = _cpu(w.q[b:b + 1, :ng * G]), _cpu(w.k[b:b + 1, :ng]), _cpu(w.v[b:b + 1, :ng])
+        t0 = time.perf_counter()
+        reference_path_sdpa(q, k, v, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin, q_pos=pos,
+                            causal=True)
+        dt += time.perf_counter() - t0
+        del q, k, v
+    frac = ng / Hkv
+    work = w.work * frac
+    out = {"value": round(work / dt / 1e12, 4), "unit": "TFLOP/s", **_host(), "kind": "port",
+           "seconds": round(dt, 3)}
+    if frac == 1.0:
+        out["sample"] = (f"the full workload ({B} batch rows, one at a time), fp32; "
+                         "QK-Norm + RoPE + repeat_interleave + SDPA")
+    else:
+        out["sample"] = (f"{ng} of {Hkv} KV groups ({ng * G} query heads x {S} rows, causal), fp32, "
+                         f"{dt:.1f} s; the full workload extrapolates x{Hkv // ng} to "
+                         f"{dt * Hkv / ng:.1f} s at the same rate")
+        out["extrapolated_full_seconds"] = round(dt * Hkv / ng, 2)
+    return out
+
+
+def cpu_decode(w, budget_s=20.0):
+    """The reference's decode step (QK-Norm + RoPE of the new token, KVCache
+    concatenation, repeat_interleave, SDPA; model/attention.py:24-46, 95-115) in
+    fp32 on the host cores, as B=1 slices with each sequence's own length, over
+    the workload's own cache contents.  Bytes are counted as on the GPU."""
+    from oracle import reference_decode_sdpa
+    Hq, Hkv, D = w.Hq, w.Hkv, w.D
+    cos, sin, one = _cpu(w.cos), _cpu(w.sin), torch.ones(D)
+    reference_decode_sdpa(torch.randn(1, Hq, 1, D), torch.randn(1, Hkv, 1, D), torch.randn(1, Hkv, 1, D),
+                          torch.randn(1, Hkv, 63, D), torch.randn(1, Hkv, 63, D), q_weight=one,
+                          k_weight=one, eps=1e-6, cos=cos, sin=sin)
+    dt, dt_gqa, nbytes, done = 0.0, 0.0, 0, 0
+    for b in range(w.B):
+        T = int(w.lens_cpu[b])
+        kc, vc = _cpu(w.kc[b:b + 1, :, :T - 1]), _cpu(w.vc[b:b + 1, :, :T - 1])
+        q, kn, vn = _cpu(w.q[b:b + 1]), _cpu(w.knew[b:b + 1]), _cpu(w.vnew[b:b + 1])
+        t0 = time.perf_counter()
+        reference_decode_sdpa(q, kn, vn, kc, vc, q_weight=one, k_weight=one, eps=1e-6, cos=cos, sin=sin)
+        t1 = time.perf_counter()
+        reference_decode_sdpa(q, kn, vn, kc, vc, q_weight=one, k_weight=one, eps=1e-6, cos=cos, sin=sin,
+                              repeat_kv=False)
+        dt_gqa += time.perf_counter() - t1
+        dt += t1 - t0
+        nbytes += 2 * Hkv * T * D * 2 + 2 * Hq * D * 2
+        done += 1
+        del kc, vc
+        if dt + dt_gqa > budget_s:
             break
-    dt = time.perf_counter() - t0
-    flops = 4.0 * D * rows * Hq * S * (S + 1) / 2
-    return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{rows} batch rows (= {rows / B:.1f} passes over the B8 batch) of "
-                      f"S2048 Hq16 Hkv8 D128 causal prefill (QK-Norm+RoPE+GQA attention, "
-                      f"fp32 torch oracle), {dt:.1f} s"}
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", **_host(), "kind": "port",
+            "seconds": round(dt, 3),
+            "sample": f"{done} of {w.B} sequences as B=1 slices with their own lengths "
+                      f"({nbytes / 1e9:.3f} GB of the workload's bf16 algorithmic bytes), fp32; "
+                      "norm + RoPE of the new token, cache concatenation, repeat_interleave, SDPA",
+            "value_sdpa_enable_gqa": round(nbytes / dt_gqa / 1e9, 3),
+            "note": "value_sdpa_enable_gqa: the same slices with SDPA grouping the heads itself "
+                    "instead of the reference's repeat_interleave copy of the cache"}
+
+
+def cpu_backward(w, rows=None):
+    """The reference's training composition of the attention core (repeat_interleave +
+    SDPA, model/attention.py:105-115) under autograd in fp32 on the host cores: the
+    forward runs untimed, the backward is timed, one batch row at a time."""
+    import torch.nn.functional as F
+    B, Hq, Hkv = w.B, w.Hq, w.Hkv
+    G = Hq // Hkv
+    nr = B if rows is None else rows
+    dt = 0.0
+    for i, b in enumerate([0] + list(range(nr))):    # pass 0 (row 0 again) warms up, untimed
+        q, k, v = (_cpu(t[b:b + 1]).requires_grad_(True) for t in (w.q, w.k, w.v))
+        do = _cpu(w.do[b:b + 1])
+        o = F.scaled_dot_product_attention(q, k.repeat_interleave(G, 1), v.repeat_interleave(G, 1),
+                                           is_causal=True)
+        t0 = time.perf_counter()
+        o.backward(do)
+        if i > 0:
+            dt += time.perf_counter() - t0
+        del q, k, v, do, o
+    work = w.work * nr / B
+    out = {"value": round(work / dt / 1e12, 4), "unit": "TFLOP/s", **_host(), "kind": "port",
+           "seconds": round(dt, 3)}
+    if nr == B:
+        out["sample"] = f"the full workload ({B} batch rows, one at a time), fp32 autograd backward"
+    else:
+        out["sample"] = (f"{nr} of {B} batch rows, fp32 autograd backward, {dt:.1f} s; the full "
+                         f"workload extrapolates x{B // nr} to {dt * B / nr:.1f} s at the same rate")
+        out["extrapolated_full_seconds"] = round(dt * B / nr, 2)
+    return out
+
+
+def cpu_baseline(name, w):
+    if name in ("c2", "c3"):
+        return cpu_prefill(w)
+    if name == "c5":
+        return cpu_prefill(w, groups=1)
+    if name == "c4":
+        return cpu_decode(w)
+    if name == "c2_bwd":
+        return cpu_backward(w)
+    if name == "c3_bwd":
+        return cpu_backward(w, rows=1)
+    return None
+
+
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over this workload's kernels, in runs of "
+                  "their own scaled by a plain-copy calibration: profiles/attention_kernels_hbm_traffic.txt "
+                  "(profile-derived, not measured in this run)")
 
 
 def main():
@@ -375,41 +486,49 @@ def main():
                             4, 8192, 32, 8, 128, seed=1006)
         raise SystemExit(f"unknown workload {name}")
 
-    results = {}
+    results, cpu = {}, {}
     for name in names:
         w = build(name)
-        steps = args.steps if name != "c5" else max(2, min(args.steps, 4))
+        # C5 takes ~0.1 s a step: at least 5 timed steps, a bounded number
+        steps = args.steps if name != "c5" else max(5, min(args.steps, 8))
         warm = args.warmup if name != "c5" else 1
         log(f"{name}: {steps} timed steps after {warm} warmup")
         step_ms, kern_ms, kern_med = time_workload(w, steps, warm)
         val, unit = w.throughput(step_ms)
-        results[name] = (w, step_ms, kern_ms, kern_med, val, unit, steps, warm)
+        results[name] = {"config": w.describe(), "value": round(val, 3), "unit": unit,
+                         "ms_per_step": round(step_ms, 5), "steps": steps, "warmup": warm,
+                         "roofline": w.roofline(kern_ms)}
         log(f"{name}: {step_ms:.4f} ms/step, kernel avg {kern_ms:.4f} ms, {val:.2f} {unit}")
-        if name != "c2":
-            del w
-            torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            log(f"{name}: cpu baseline (the reference's composition in fp32 on the host cores)")
+            cpu[name] = cpu_baseline(name, w)
+            if cpu[name] is not None:
+                log(f"{name}: cpu {cpu[name]['value']} {cpu[name]['unit']} in {cpu[name]['seconds']} s")
+        del w
+        torch.cuda.empty_cache()
 
     traffic = measured_traffic()
-    w, step_ms, kern_ms, kern_med, val, unit, steps, warm = results["c2"]
+    for name, r in results.items():
+        r["roofline"]["traffic"] = traffic.get(name)
+        r["roofline"]["traffic_source"] = TRAFFIC_SOURCE if name in traffic else None
+        if name == "c4_paged" and "c4" in cpu:
+            r["cpu_baseline"] = dict(cpu["c4"], sample="the c4 sequences (the reference has no "
+                                     "paged cache): " + cpu["c4"]["sample"])
+        elif cpu.get(name) is not None:
+            r["cpu_baseline"] = cpu[name]
+    head = results.pop("c2")
     line = {
-        "metric": METRIC, "value": round(val, 3), "unit": unit, "n_gpus": 1,
-        "steps": steps, "warmup": warm, "ms_per_step": round(step_ms, 5),
+        "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1,
+        "steps": head["steps"], "warmup": head["warmup"], "ms_per_step": head["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) inputs, QK-Norm weights 1+0.02*N(0,1))",
-        "config": w.describe(),
-        "roofline": w.roofline(kern_ms, traffic.get("c2")),
+        "config": head["config"], "roofline": head["roofline"],
     }
-    sec = {}
-    for name, (w2, sms, kms, kmed, v2, u2, st2, wu2) in results.items():
-        if name == "c2":
-            continue
-        sec[name] = {"config": w2.describe(), "value": round(v2, 3), "unit": u2,
-                     "ms_per_step": round(sms, 5), "steps": st2,
-                     "roofline": w2.roofline(kms, traffic.get(name))}
-    line["secondary"] = sec
-    if not args.no_cpu_baseline:
-        log("cpu baseline (oracle on host cores)")
-        line["cpu_baseline"] = cpu_baseline()
+    for r in results.values():
+        r.pop("warmup")
+    line["secondary"] = results
+    if "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
     print(json.dumps(line), flush=True)
 
 

@@ -15,6 +15,8 @@ from .attention_oracle import (  # noqa: F401
     rotate_half,
     attention,
     attention_path,
+    reference_path_sdpa,
+    reference_decode_sdpa,
     decode_path,
     attention_module_forward,
     OracleKVCache,

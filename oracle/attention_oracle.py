@@ -31,6 +31,14 @@ Pinning status (what checks each function, see tests/test_oracle_*.py):
                          prefill + decode protocol, bf16 module).
   * decode_path       -- equals the last row of a causal prefill over the same
                          keys; ragged rows equal their B=1 slices.
+  * reference_path_sdpa -- the reference's composition with torch SDPA (the
+                         CPU baseline's timed routine): equals attention_path
+                         (golden-pinned) on seeded inputs, causal and not,
+                         S == T and S < T.
+  * reference_decode_sdpa -- the reference's decode step with SDPA (the
+                         decode CPU baseline): equals decode_path over the
+                         grown cache, and its appended row is the k-hat of
+                         attention_path at that position.
 """
 
 from __future__ import annotations
@@ -49,6 +57,8 @@ __all__ = [
     "rotate_half",
     "attention",
     "attention_path",
+    "reference_path_sdpa",
+    "reference_decode_sdpa",
     "decode_path",
     "attention_module_forward",
     "OracleKVCache",
@@ -242,6 +252,77 @@ def attention_path(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     o = attention(qh, kh, v, causal=causal, causal_offset=causal_offset, scale=scale,
                   compute_dtype=compute_dtype, q_block=q_block)
     return (o, kh) if return_khat else o
+
+
+def reference_path_sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                        q_weight: Optional[torch.Tensor], k_weight: Optional[torch.Tensor],
+                        eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                        q_pos: torch.Tensor, k_pos: Optional[torch.Tensor] = None,
+                        causal: bool = True) -> torch.Tensor:
+    """The reference's own composition of the post-projection path, as the CPU
+    baseline times it: QK-Norm (norm.py:17-22), rotate-half RoPE from the fp32
+    tables (rope.py:133-161), ``repeat_interleave`` of the KV heads
+    (attention.py:105-108) and ``F.scaled_dot_product_attention``
+    (attention.py:110-115), all in the inputs' dtype.  Causal with S < T is
+    bottom-right aligned (an explicit mask, since SDPA's is_causal is
+    top-left).  Pinned against ``attention_path`` in the oracle tests.
+    """
+    import torch.nn.functional as F
+    if k_pos is None:
+        k_pos = q_pos
+    if q_weight is not None:
+        q = rms_norm(q, q_weight, eps)
+    if k_weight is not None:
+        k = rms_norm(k, k_weight, eps)
+    q = rotate_half(q, _gather_table(cos, q_pos), _gather_table(sin, q_pos))
+    k = rotate_half(k, _gather_table(cos, k_pos), _gather_table(sin, k_pos))
+    G = q.shape[1] // k.shape[1]
+    if G > 1:
+        k = k.repeat_interleave(G, dim=1)
+        v = v.repeat_interleave(G, dim=1)
+    S, T = q.shape[2], k.shape[2]
+    if causal and S != T:
+        keep = torch.ones(S, T, dtype=torch.bool).tril(T - S)
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=keep)
+    return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+
+def reference_decode_sdpa(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                          k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+                          q_weight: Optional[torch.Tensor], k_weight: Optional[torch.Tensor],
+                          eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                          repeat_kv: bool = True):
+    """One decode step of the reference, as the CPU baseline times it, for one
+    sequence: QK-Norm and RoPE of the new token at position ``T - 1``
+    (attention.py:95-100), the cache's concatenation (KVCache.update,
+    attention.py:35-44), ``repeat_interleave`` (attention.py:105-108) and SDPA
+    with no mask (attention.py:110-115).
+
+    q: (1, Hq, 1, D), k_new/v_new: (1, Hkv, 1, D) pre-norm projections;
+    k_cache/v_cache: (1, Hkv, T - 1, D) holding earlier K-hat and V.  Returns
+    (o (1, Hq, 1, D), k_all, v_all) with the grown cache.  Pinned against
+    ``decode_path`` in the oracle tests.  ``repeat_kv=False`` lets SDPA group
+    the heads itself (``enable_gqa``) instead of materialising the repeated
+    cache: the same function without the reference's copy.
+    """
+    import torch.nn.functional as F
+    pos = torch.tensor([k_cache.shape[2]])
+    if q_weight is not None:
+        q = rms_norm(q, q_weight, eps)
+    if k_weight is not None:
+        k_new = rms_norm(k_new, k_weight, eps)
+    c, s_ = _gather_table(cos, pos), _gather_table(sin, pos)
+    q, k_new = rotate_half(q, c, s_), rotate_half(k_new, c, s_)
+    k_all = torch.cat([k_cache, k_new], dim=2)
+    v_all = torch.cat([v_cache, v_new], dim=2)
+    G = q.shape[1] // k_all.shape[1]
+    k, v = k_all, v_all
+    if G > 1 and not repeat_kv:
+        return F.scaled_dot_product_attention(q, k, v, enable_gqa=True), k_all, v_all
+    if G > 1:
+        k = k.repeat_interleave(G, dim=1)
+        v = v.repeat_interleave(G, dim=1)
+    return F.scaled_dot_product_attention(q, k, v), k_all, v_all
 
 
 def decode_path(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

@@ -12,8 +12,9 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle import (attention, attention_path, decode_path, rms_norm, rope_inv_freq,
-                    rope_tables, rotate_half, yarn_correction_range, yarn_inv_freq)
+from oracle import (attention, attention_path, decode_path, reference_decode_sdpa, reference_path_sdpa,
+                    rms_norm, rope_inv_freq, rope_tables, rotate_half, yarn_correction_range,
+                    yarn_inv_freq)
 
 
 def _rand(*shape, seed=0, dtype=torch.float64):
@@ -221,3 +222,61 @@ def test_decode_ragged_rows_equal_their_slices():
     torch.testing.assert_close(again, full, rtol=0, atol=0)
     # length-1 row returns V[0] for every head
     torch.testing.assert_close(full[2], vc[2, 0, 0].expand(Hq, D), rtol=1e-14, atol=1e-14)
+
+
+# ---------------------------------------------------------------- the CPU baseline's routine
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("S,T", [(37, 37), (9, 40)])
+def test_reference_path_sdpa_equals_attention_path(causal, S, T):
+    """The timed CPU baseline (QK-Norm -> RoPE -> repeat_interleave -> SDPA) computes
+    the same function as the golden-pinned attention_path, including bottom-right
+    causal alignment when the queries are the last S of T positions."""
+    B, Hq, Hkv, D = 2, 8, 2, 32
+    q, k, v = _rand(B, Hq, S, D, seed=61), _rand(B, Hkv, T, D, seed=62), _rand(B, Hkv, T, D, seed=63)
+    qw, kw = 1 + 0.1 * _rand(D, seed=64), 1 + 0.1 * _rand(D, seed=65)
+    cos, sin = rope_tables(D, 64, 1e6)
+    cos, sin = cos.double(), sin.double()
+    qpos, kpos = torch.arange(T - S, T), torch.arange(T)
+    got = reference_path_sdpa(q, k, v, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin,
+                              q_pos=qpos, k_pos=kpos, causal=causal)
+    ref = attention_path(q, k, v, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin, q_pos=qpos,
+                         k_pos=kpos, causal=causal, causal_offset=T - S if causal else 0,
+                         compute_dtype=torch.float64)
+    # QK-Norm upcasts to fp32 as the reference does (norm.py:20), so fp64 inputs
+    # differ from the fp64 oracle by fp32 rounding (~3e-7); a wrong term is O(0.1)
+    torch.testing.assert_close(got, ref, rtol=1e-5, atol=1e-6)
+    # the first query of a causal S < T block still sees T - S + 1 keys, not one
+    if causal and S < T:
+        one = reference_path_sdpa(q, k[:, :, :1], v[:, :, :1], q_weight=qw, k_weight=kw, eps=1e-6,
+                                  cos=cos, sin=sin, q_pos=qpos[:1], k_pos=kpos[:1], causal=True)
+        assert not torch.allclose(got[:, :, :1], one[:, :, :1])
+
+
+def test_reference_decode_sdpa_equals_decode_path():
+    """The decode CPU baseline's step (norm + RoPE of the new token, cache concatenation,
+    repeat_interleave, SDPA) equals decode_path over the grown cache, and the row it
+    appends is attention_path's k-hat at that position."""
+    Hq, Hkv, D, T = 8, 2, 32, 23
+    q, kn, vn = _rand(1, Hq, 1, D, seed=71), _rand(1, Hkv, 1, D, seed=72), _rand(1, Hkv, 1, D, seed=73)
+    kc, vc = _rand(1, Hkv, T - 1, D, seed=74), _rand(1, Hkv, T - 1, D, seed=75)
+    qw, kw = 1 + 0.1 * _rand(D, seed=76), 1 + 0.1 * _rand(D, seed=77)
+    cos, sin = rope_tables(D, 64, 1e6)
+    cos, sin = cos.double(), sin.double()
+    o, k_all, v_all = reference_decode_sdpa(q, kn, vn, kc, vc, q_weight=qw, k_weight=kw, eps=1e-6,
+                                            cos=cos, sin=sin)
+    assert k_all.shape == (1, Hkv, T, D)
+    torch.testing.assert_close(k_all[:, :, :T - 1], kc, rtol=0, atol=0)
+    torch.testing.assert_close(v_all[:, :, -1:], vn, rtol=0, atol=0)
+    _, kh = attention_path(q, kn, vn, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin,
+                           q_pos=torch.tensor([T - 1]), causal=False, compute_dtype=torch.float64,
+                           return_khat=True)
+    # fp32 QK-Norm as in the reference (norm.py:20): fp32 rounding, a wrong term is O(0.1)
+    torch.testing.assert_close(k_all[:, :, -1:], kh, rtol=1e-5, atol=1e-6)
+    ref = decode_path(q[:, :, 0], k_all, v_all, torch.tensor([T], dtype=torch.int32), q_weight=qw,
+                      eps=1e-6, cos=cos, sin=sin, q_pos=torch.tensor([T - 1]),
+                      compute_dtype=torch.float64)
+    torch.testing.assert_close(o[:, :, 0], ref, rtol=1e-5, atol=1e-6)
+    og, _, _ = reference_decode_sdpa(q, kn, vn, kc, vc, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos,
+                                     sin=sin, repeat_kv=False)
+    torch.testing.assert_close(og, o, rtol=1e-12, atol=1e-12)
