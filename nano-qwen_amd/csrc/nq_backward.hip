@@ -15,8 +15,9 @@
 // owns the G heads x BM positions of one kv head and walks the key tiles; it
 // also forms each row's Delta and stores it with the row's LSE for the next
 // kernel); dK/dV per key block (a workgroup owns 128 keys of one kv head and
-// walks every query row of its G heads, so the GQA sum over heads happens in
-// registers, with no atomics).
+// walks every query row of its G heads, last query tile first, so the GQA sum
+// over heads happens in registers, with no atomics, and the key blocks of a
+// pair stream Q / dO through L2 together).
 //
 // MFMA layouts (v_mfma_f32_32x32x16_bf16): A lane l holds row l%32, k = 8*(l/32)..+7;
 // B lane l holds column l%32, the same k; C lane l holds column l%32, rows
@@ -319,7 +320,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   const int Tk = bw_keys(p, b);  // keys past Tk are padding: zero gradients, rows never read
   const int key_c = key < Tk ? key : k0;  // a padded key's K row: the block's first (read only if < Tk)
 
-  // the work list: (head g, query tile qt) for queries that see a key of this
+  // the work list: (query tile qt, head g) for queries that see a key of this
   // block (q + coff >= k0); none when the whole block is padding
   const int qstart = CAUSAL ? max(0, k0 - p.coff) / BW_BQ * BW_BQ : 0;
   const int nqt = (qstart < p.S && k0 < Tk) ? (p.S - qstart + BW_BQ - 1) / BW_BQ : 0;
@@ -359,15 +360,20 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
     if (wave == 3 && lane < 16)
       global_load_lds16(p.ws + bw_ws_index(p, b, head, qt) + lane * 4, base + 2 * TB);
   };
-  // steps run head by head, query tile by query tile
+  // Steps run query tile by query tile from the LAST tile down to qstart, the
+  // G heads of a tile back to back.  Every key block of a pair then starts at
+  // the same tile and walks down in step with the others (they only differ in
+  // where they stop), so the workgroups of one pair that are resident on an
+  // XCD read each Q / dO tile at about the same time and share it in L2,
+  // instead of streaming windows of the pair offset by their key blocks.
   auto advance = [&](int& g, int& qt) {
-    qt += BW_BQ;
-    if (qt >= p.S) {
-      qt = qstart;
-      ++g;
+    if (++g == p.G) {
+      g = 0;
+      qt -= BW_BQ;
     }
   };
-  int gn = 0, qtn = qstart;  // the next step to stage
+  const int qtop = qstart + (nqt - 1) * BW_BQ;  // the last query tile
+  int gn = 0, qtn = qtop;  // the next step to stage
   // V of the block's keys stays in LDS (read as the B operand of dP each
   // step); K of the lane's key is held in registers (B operand of S).  Both
   // stagings are waited for at the top of the first iteration (a workgroup
@@ -410,13 +416,10 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd) dkacc[dd] = dvacc[dd] = floatx16{};
 
-  int qnext = qstart;
+  int gcur = 0, qnext = qtop;
   for (int it = 0; it < niter; ++it) {
     const int qt = qnext;  // this step's query tile
-    {
-      int g_unused = 0;
-      advance(g_unused, qnext);
-    }
+    advance(gcur, qnext);
     wait_vmcnt0();  // the LSE / Delta rows always come through global_load_lds
     __syncthreads();
     if (it + 1 < niter) {

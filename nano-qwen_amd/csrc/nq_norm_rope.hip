@@ -13,9 +13,12 @@
 // row owns elements [8s, 8s+8) and their RoPE partners [D/2+8s, D/2+8s+8)
 // (two 16-byte bf16 loads), so the rotation needs no cross-lane traffic; the
 // norm's sum of squares is reduced over the row's lanes with DPP adds
-// (row_half_mirror, then quad swaps), all VALU.  The grid is capped at 4
-// blocks per CU and loops over rows; in large launches each thread takes two
-// rows per step so that four row loads are in flight.  HBM-bound: one read and
+// (row_half_mirror, then quad swaps), all VALU.  Rows are enumerated with the
+// heads of one position adjacent when the source stores them so (a wave then
+// reads contiguous memory and its rows share their cos/sin table rows, which
+// matters when the tables outgrow the L2), else position-fastest.  The grid
+// is capped at 4 blocks per CU and loops over rows; in large launches each
+// thread takes two rows per step so that four row loads are in flight.  HBM-bound: one read and
 // one write per element; the weight and table reads hit the caches.
 
 #include "nq_common.hpp"
@@ -33,6 +36,7 @@ struct RowJob {
   int rope;             // apply RoPE
   int norm;             // apply RMSNorm
   int use_row_base;     // destination row = row_base[b] + s
+  int heads_inner;      // source heads closer in memory than positions: rows run (b, s, h), h fastest
 };
 
 struct RowParams {
@@ -56,8 +60,14 @@ struct RowParams {
   int page_size;
 };
 
-constexpr int ROW_MAX_BLOCKS = 1024;  // grid cap: 4 blocks per CU on 256 CUs, looping over rows
-constexpr int64_t ROW_UNROLL_MIN = 32768;  // rows per job from which each thread takes two
+#ifndef NQ_ROW_MAX_BLOCKS
+#define NQ_ROW_MAX_BLOCKS 1024
+#endif
+#ifndef NQ_ROW_UNROLL_MIN
+#define NQ_ROW_UNROLL_MIN 32768
+#endif
+constexpr int ROW_MAX_BLOCKS = NQ_ROW_MAX_BLOCKS;  // grid cap: 4 blocks per CU on 256 CUs, looping over rows
+constexpr int64_t ROW_UNROLL_MIN = NQ_ROW_UNROLL_MIN;  // rows per job from which each thread takes two
 
 template <typename TI, typename TO, int D, int ROW_UNROLL>
 __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
@@ -84,11 +94,21 @@ __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
   for (int u = 0; u < ROW_UNROLL; ++u) {
     const int64_t row = row0 + u * RPB;
     act[u] = row < nrows;
-    // row -> (b, h, s) with s fastest
-    const int64_t rr = act[u] ? row : 0;
-    ss_[u] = (int)(rr % p.S);
-    hh[u] = (int)((rr / p.S) % jb.H);
-    bb[u] = (int)(rr / ((int64_t)p.S * jb.H));
+    // row -> (b, h, s): s fastest, or h fastest when the heads of one position
+    // are adjacent in memory (the projections' (B, S, H, D) storage): a wave
+    // then reads contiguous bytes and its rows share table rows
+    const uint32_t rr = act[u] ? (uint32_t)row : 0u;
+    if (jb.heads_inner) {
+      hh[u] = (int)(rr % (uint32_t)jb.H);
+      const uint32_t t = rr / (uint32_t)jb.H;
+      ss_[u] = (int)(t % (uint32_t)p.S);
+      bb[u] = (int)(t / (uint32_t)p.S);
+    } else {
+      ss_[u] = (int)(rr % (uint32_t)p.S);
+      const uint32_t t = rr / (uint32_t)p.S;
+      hh[u] = (int)(t % (uint32_t)jb.H);
+      bb[u] = (int)(t / (uint32_t)jb.H);
+    }
     const TI* src = reinterpret_cast<const TI*>(jb.src) + bb[u] * jb.sb + hh[u] * jb.sh + ss_[u] * jb.ss + sub * 8;
     x1[u] = act[u] ? Vec8<TI>::load_f32(src) : floatx8{};
     x2[u] = act[u] ? Vec8<TI>::load_f32(src + D / 2) : floatx8{};
@@ -118,10 +138,14 @@ template <typename TI, typename TO, int D>
 static hipError_t launch_rows(const RowParams& p, int max_h, hipStream_t st) {
   constexpr int RPB = (64 / (D / 16)) * 4;  // rows per block and row step
   const int64_t nrows = (int64_t)p.B * max_h * p.S;
-  const int u = nrows >= ROW_UNROLL_MIN ? 2 : 1;
+#ifndef NQ_ROW_UNROLL_BIG
+#define NQ_ROW_UNROLL_BIG 2
+#endif
+  const int u = nrows >= ROW_UNROLL_MIN ? NQ_ROW_UNROLL_BIG : 1;
   const int64_t blocks = (nrows + RPB * u - 1) / (RPB * u);
   dim3 grid((unsigned)(blocks < ROW_MAX_BLOCKS ? blocks : ROW_MAX_BLOCKS), (unsigned)p.njobs);
-  if (u == 2) hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 2>), grid, dim3(256), 0, st, p);
+  if (u == 4) hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 4>), grid, dim3(256), 0, st, p);
+  else if (u == 2) hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 2>), grid, dim3(256), 0, st, p);
   else hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 1>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
@@ -175,9 +199,12 @@ static int qk_norm_rope_impl(const void* q, const int64_t* q_strides, void* q_ou
     j.db = in.ds[0]; j.dh = in.ds[1]; j.ds = in.ds[2];
     j.weight = in.w; j.H = in.H; j.rope = in.rope && cos_tab != nullptr; j.norm = in.w != nullptr;
     j.use_row_base = in.rb;
+    j.heads_inner = in.H > 1 && S > 1 && (in.ss[1] < 0 ? -in.ss[1] : in.ss[1]) < (in.ss[2] < 0 ? -in.ss[2] : in.ss[2]);
     if (in.H > max_h) max_h = in.H;
   }
   if (nj == 0) return NQ_OK;
+  if ((int64_t)B * max_h * S >= (1LL << 31))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "B * heads * S must stay below 2^31 rows");
   p.njobs = nj;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
