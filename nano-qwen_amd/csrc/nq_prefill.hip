@@ -144,7 +144,7 @@ prefill_kernel(PrefillParams p) {
   if (Tk <= 0) {  // no keys: zeros; a length out of range: NaN
     const float f = Tk < 0 ? __builtin_nanf("") : 0.f;
     for (int r = threadIdx.x; r < 32 * NW; r += 64 * NW) {
-      const int g = r / p.BM, qi = q0 + r - g * p.BM;
+      const int g = r % p.G, qi = q0 + r / p.G;
       if (qi >= p.S) continue;
       T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (kvh * p.G + g) * p.osh + (int64_t)qi * p.oss;
       for (int d = 0; d < D; ++d) orow[d] = (T)f;
@@ -207,54 +207,75 @@ prefill_kernel(PrefillParams p) {
   };
   auto load_k = [&](int tile, int buf) { load_tile(kbase, krow_bytes, koff, buf * TB, tile); };
   auto load_v = [&](int tile, int buf) { load_tile(vbase, vrow_bytes, voff, (2 + buf) * TB, tile); };
-  // issue the first tiles before the Q work so their latency overlaps it
-  load_k(0, 0);
-  load_v(0, 0);
-  if (ntiles > 1) load_k(1, 1);
-
-  // this lane's query row: column r32 of this wave's 32 rows
+  // this lane's query row: column r32 of this wave's 32 rows.  Row R of the
+  // workgroup is head R % G at position q0 + R / G: the G heads of a position
+  // sit in adjacent lanes, so a wave's rows span 32 / G positions and their
+  // cos/sin table rows (and, in the projections' (B, S, H, D) storage, their
+  // Q and O rows) share cache lines.
   const int R = wave * 32 + r32;
-  const int g = R / p.BM, pr = R - g * p.BM;
+  const int g = R % p.G, pr = R / p.G;
   const int head = kvh * p.G + g;
   const int qi = q0 + pr;
   const bool qvalid = qi < p.S;
   const int qi_c = qvalid ? qi : p.S - 1;
 
+  // ---- prologue loads.  The first K/V tiles go first, then every register
+  // load of the Q work (the Q row, the norm weight, the row's cos/sin) back to
+  // back, so that a single memory round trip covers all of them before the Q
+  // work starts (each load depending on an earlier one's result would cost a
+  // round trip of its own).  The table row is resolved before anything is in
+  // flight: only explicit per-token positions need a load for it.
+  const bool do_norm = FUSE_Q && p.qw != nullptr;
+  const bool do_rope = FUSE_Q && p.cos_tab != nullptr;
+  int tab_row = 0;
+  if (do_rope) tab_row = table_row(row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S), p.max_pos);
+  load_k(0, 0);
+  load_v(0, 0);
+  if (ntiles > 1) load_k(1, 1);
+  floatx8 xf[NDB];
+  floatx8 wq[NDB];
+  floatx8 tc[NDB / 2], ts[NDB / 2];
+  {
+    const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qi_c * p.qss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) xf[db] = Vec8<T>::load_f32(qrow + db * 16 + hh * 8);
+    if (do_norm) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) wq[db] = Vec8<float>::load_f32(p.qw + db * 16 + hh * 8);
+    }
+    if (do_rope) {
+#pragma unroll
+      for (int db = 0; db < NDB / 2; ++db) {
+        tc[db] = load_tab8(p.cos_tab, tab_row, D / 2, db * 16 + hh * 8);
+        ts[db] = load_tab8(p.sin_tab, tab_row, D / 2, db * 16 + hh * 8);
+      }
+    }
+  }
+
   // ---- Q operand (B of S^T = K Q^T): lane holds Q[row][dblk*16 + hh*8 + e]
   bf16x8 qop[NDB];
   {
-    const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qi_c * p.qss;
-    floatx8 xf[NDB];
+    if (do_norm) {
+      float ss = 0.f;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) xf[db] = Vec8<T>::load_f32(qrow + db * 16 + hh * 8);
-    if (FUSE_Q) {
-      if (p.qw) {
-        float ss = 0.f;
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int e = 0; e < 8; ++e) ss += xf[db][e] * xf[db][e];
+      ss = xor32_sum(ss);
+      const float r = rsqrtf(ss / (float)D + p.eps);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ss += xf[db][e] * xf[db][e];
-        ss = xor32_sum(ss);
-        const float r = rsqrtf(ss / (float)D + p.eps);
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          floatx8 w = Vec8<float>::load_f32(p.qw + db * 16 + hh * 8);
+        for (int e = 0; e < 8; ++e) xf[db][e] = xf[db][e] * r * wq[db][e];
+    }
+    if (do_rope) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xf[db][e] = xf[db][e] * r * w[e];
-        }
-      }
-      if (p.cos_tab) {
-        const int pos = table_row(row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S), p.max_pos);
+      for (int db = 0; db < NDB / 2; ++db) {
+        floatx8 x1 = xf[db], x2 = xf[db + NDB / 2];
 #pragma unroll
-        for (int db = 0; db < NDB / 2; ++db) {
-          floatx8 c = load_tab8(p.cos_tab, pos, D / 2, db * 16 + hh * 8);
-          floatx8 s = load_tab8(p.sin_tab, pos, D / 2, db * 16 + hh * 8);
-          floatx8 x1 = xf[db], x2 = xf[db + NDB / 2];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            xf[db][e] = x1[e] * c[e] - x2[e] * s[e];
-            xf[db + NDB / 2][e] = x2[e] * c[e] + x1[e] * s[e];
-          }
+        for (int e = 0; e < 8; ++e) {
+          xf[db][e] = x1[e] * tc[db][e] - x2[e] * ts[db][e];
+          xf[db + NDB / 2][e] = x2[e] * tc[db][e] + x1[e] * ts[db][e];
         }
       }
     }

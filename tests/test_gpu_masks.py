@@ -48,12 +48,15 @@ def test_prefill_key_lens(dtype, D, Hq, Hkv):
     torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=0, atol=tol)
 
 
-def test_prefill_key_lens_zero_and_out_of_range():
-    """0 keys: zero rows; a count outside [0, T]: NaN rows (lse -inf)."""
-    say("prefill key_lens edge values")
-    B, S, H, D = 3, 40, 4, 64
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 2)])
+def test_prefill_key_lens_zero_and_out_of_range(Hq, Hkv):
+    """0 keys: zero rows; a count outside [0, T]: NaN rows (lse -inf), for every
+    head of the group."""
+    say(f"prefill key_lens edge values {Hq}/{Hkv}")
+    B, S, D = 3, 40, 64
     lens = torch.tensor([0, 41, 40], dtype=torch.int32)
-    q, k, v = (randn(B, H, S, D, seed=710 + i, dtype=torch.bfloat16).to(DEV) for i in range(3))
+    q = randn(B, Hq, S, D, seed=710, dtype=torch.bfloat16).to(DEV)
+    k, v = (randn(B, Hkv, S, D, seed=711 + i, dtype=torch.bfloat16).to(DEV) for i in range(2))
     o, lse = ops.attention_prefill(q, k, v, causal=False, key_lens=lens.to(DEV), return_lse=True)
     o = o.float().cpu()
     assert not o[0].abs().any() and torch.isnan(o[1]).all() and torch.isfinite(o[2]).all()
