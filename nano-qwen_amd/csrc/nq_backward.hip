@@ -45,6 +45,7 @@ constexpr int BW_BN = 64;     // keys per tile (dQ kernel)
 constexpr int BW_BQ = 32;     // query rows per tile (dK/dV kernel)
 constexpr int BW_KEYS = 128;  // keys per dK/dV workgroup (32 per wave)
 constexpr int64_t BW_DQ_WIDE_MIN_WGS = 2048;  // 8-wave dQ workgroups needed to prefer them
+constexpr int BW_XCD_MIN_BLOCKS = 64;  // blocks per pair from which each XCD takes whole pairs
 
 __device__ __forceinline__ int bw_perm32(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 // C element i of a lane in half hh -> index (key or query) within its 32-block
@@ -114,7 +115,20 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r32 = lane & 31, hh = lane >> 5;
   const int npairs = p.B * p.Hkv;
-  const int qrank = blockIdx.x / npairs, pair = blockIdx.x % npairs;
+  // workgroup -> (pair, q-block), heaviest q-blocks first.  Dispatch deals
+  // workgroups to the 8 XCDs round-robin; when the pairs split evenly over
+  // them and each pair has many q-blocks, XCD x works through its own pairs
+  // one after another, so a pair's K/V stream stays in that XCD's L2
+  // (8B-like shape: HBM fetch 1.97 -> 1.15 GB per launch, time unchanged).
+  int qrank, pair;
+  if (npairs % 8 == 0 && p.nqb >= BW_XCD_MIN_BLOCKS) {
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+    pair = (k / p.nqb) * 8 + x;
+    qrank = k % p.nqb;
+  } else {
+    qrank = blockIdx.x / npairs;
+    pair = blockIdx.x % npairs;
+  }
   const int qblk = CAUSAL ? (p.nqb - 1 - qrank) : qrank;
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int q0 = qblk * p.BM;
@@ -307,13 +321,27 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r32 = lane & 31, hh = lane >> 5;
-  // key blocks in launch order across all (batch, kv head) pairs: under the
-  // causal mask the first keys see the most queries, so the heaviest blocks
-  // start first.  Consecutive blocks are different pairs: with a pair count
-  // that is a multiple of 8, a pair's blocks all land on one XCD (dispatch is
-  // round-robin over the 8) and share its L2 for the Q / dO stream.
+  // key blocks in launch order: under the causal mask the first keys see the
+  // most queries, so the heaviest blocks start first.  Dispatch deals
+  // workgroups to the 8 XCDs round-robin.  When the pairs split evenly over
+  // the XCDs and each has many key blocks, XCD x works through its own pairs
+  // one at a time, so the blocks of one pair are co-resident and walk the
+  // query tiles together, sharing its L2 for the Q / dO stream (8B-like
+  // shape: HBM fetch 7.3 -> 3.7 GB per launch, time unchanged).  Otherwise
+  // consecutive blocks are different pairs, heaviest blocks of every pair
+  // first; with a pair count that is a multiple of 8 a pair's blocks still
+  // land on one XCD.
   const int npairs = p.B * p.Hkv;
-  const int kblk = blockIdx.x / npairs, pair = blockIdx.x % npairs;
+  int kblk, pair;
+  const int nkb = gridDim.x / npairs;
+  if (npairs % 8 == 0 && nkb >= BW_XCD_MIN_BLOCKS) {
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+    pair = (k / nkb) * 8 + x;
+    kblk = k % nkb;
+  } else {
+    kblk = blockIdx.x / npairs;
+    pair = blockIdx.x % npairs;
+  }
   const int b = pair / p.Hkv, kvh = pair % p.Hkv;
   const int k0 = kblk * BW_KEYS;
   const int key = k0 + wave * 32 + r32;  // this lane's key (C column)
