@@ -526,18 +526,41 @@ prefill_kernel(PrefillParams p) {
   }
 
   l_i = xor32_sum(l_i);
-  if (!qvalid) return;
   const float inv_l = 1.f / l_i;
-  T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + head * p.osh + (int64_t)qi * p.oss;
+
+  // ---- epilogue: O goes through LDS, so that every store instruction writes
+  // whole rows (16 lanes x 16 contiguous bytes per row) instead of 8-byte
+  // pieces of 32 rows, which leave L2 as partly written lines.  Each wave
+  // stages its own 32 rows in its own slice of the (now idle) tile buffers,
+  // with the K tile's chunk swizzle, and reads them back row-major.
+  static_assert(std::is_same<T, bf16>::value, "bf16 output");
+  constexpr int OCH = D / 8;  // 16-byte chunks per output row
+  static_assert(32 * NW * Tl::ROW_BYTES <= 4 * TB, "output stage fits the tile buffers");
+  __syncthreads();  // every wave is done with the last K/V tiles
+  unsigned char* const ostage = smem + wave * 32 * Tl::ROW_BYTES;
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      floatx4 t = {oacc[dd][gq * 4 + 0] * inv_l, oacc[dd][gq * 4 + 1] * inv_l,
-                   oacc[dd][gq * 4 + 2] * inv_l, oacc[dd][gq * 4 + 3] * inv_l};
-      store4<T>(orow + dd * 32 + gq * 8 + hh * 4, t);
+      const floatx4 t = {oacc[dd][gq * 4 + 0] * inv_l, oacc[dd][gq * 4 + 1] * inv_l,
+                         oacc[dd][gq * 4 + 2] * inv_l, oacc[dd][gq * 4 + 3] * inv_l};
+      *reinterpret_cast<bf16x4*>(ostage + r32 * Tl::ROW_BYTES + Tl::k_chunk(r32, dd * 4 + gq) * 16 + hh * 8) =
+          __builtin_convertvector(t, bf16x4);
     }
-  if (p.lse && hh == 0) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = (m_i + __log2f(l_i)) * kLn2;
+  {
+    constexpr int RPR = 64 / OCH;  // rows per read-back instruction
+#pragma unroll
+    for (int i = 0; i < 32 / RPR; ++i) {
+      const int r = i * RPR + lane / OCH, c = lane % OCH;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(ostage + r * Tl::ROW_BYTES + Tl::k_chunk(r, c) * 16);
+      const int Rw = wave * 32 + r;
+      const int qr = q0 + Rw / p.G;
+      if (qr < p.S)
+        *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.o) + b * p.osb + (kvh * p.G + Rw % p.G) * p.osh +
+                                   (int64_t)qr * p.oss + c * 8) = v;
+    }
+  }
+  if (p.lse && hh == 0 && qvalid) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = (m_i + __log2f(l_i)) * kLn2;
 }
 
 template <int D, typename T, int NW>
