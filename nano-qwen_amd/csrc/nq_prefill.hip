@@ -110,8 +110,8 @@ prefill_kernel(PrefillParams p) {
   constexpr int NDB = D / 16;        // 16-wide d blocks (QK^T k-steps)
   constexpr int NDO = D / 32;        // 32-wide d blocks (output tiles)
   constexpr int TB = Tl::TILE_BYTES;
-  // LDS: K0 K1 V0 V1
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TB];
+  // LDS: K0 K1 V0 V1, and one more tile's worth for the staged sin rows
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[5 * TB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -229,9 +229,28 @@ prefill_kernel(PrefillParams p) {
   const bool do_rope = FUSE_Q && p.cos_tab != nullptr;
   int tab_row = 0;
   if (do_rope) tab_row = table_row(row_position(p.q_pos, p.q_pos_base, p.q_pos0, b, qi_c, p.S), p.max_pos);
+  // The cos/sin rows of the workgroup's BM consecutive positions are staged in
+  // LDS (cos in the V1 buffer, idle until step 0, sin in the extra tile) with
+  // coalesced 1 KiB DMA instructions, instead of every lane loading its own
+  // row's 64 values: a table row (D/2 fp32) is as long as a K row, so BM <= 64
+  // rows fit one tile.  Explicit per-token positions keep the per-lane loads.
+  const bool stage_tab = do_rope && p.q_pos == nullptr && p.BM <= PF_BN;
   load_k(0, 0);
   load_v(0, 0);
   if (ntiles > 1) load_k(1, 1);
+  if (stage_tab) {
+    const int pos0 = (p.q_pos_base ? p.q_pos_base[b] : p.q_pos0) + q0;
+    constexpr int TROW = D * 2;  // bytes per table row
+    const int ninst = (p.BM * TROW + 1023) / 1024;
+    for (int m = wave; m < ninst; m += NW) {
+      const int pb = m * 1024 + lane * 16;
+      const int row = pb / TROW;
+      const int c = Tl::k_chunk(row, (pb % TROW) / 16);  // logical 16-byte chunk (4 values)
+      const int tr = min(max(pos0 + min(row, p.BM - 1), 0), p.max_pos - 1);
+      global_load_lds16(p.cos_tab + (int64_t)tr * (D / 2) + c * 4, smem + 3 * TB + m * 1024);
+      global_load_lds16(p.sin_tab + (int64_t)tr * (D / 2) + c * 4, smem + 4 * TB + m * 1024);
+    }
+  }
   floatx8 xf[NDB];
   floatx8 wq[NDB];
   floatx8 tc[NDB / 2], ts[NDB / 2];
@@ -244,10 +263,28 @@ prefill_kernel(PrefillParams p) {
       for (int db = 0; db < NDB; ++db) wq[db] = Vec8<float>::load_f32(p.qw + db * 16 + hh * 8);
     }
     if (do_rope) {
+      if (stage_tab) {
+        wait_vmcnt0();
+        __syncthreads();
+        // row pr of the stage; a position outside the tables gives NaN, as the
+        // per-lane loads do
+        const float bad = tab_row < 0 ? __builtin_nanf("") : 0.f;
 #pragma unroll
-      for (int db = 0; db < NDB / 2; ++db) {
-        tc[db] = load_tab8(p.cos_tab, tab_row, D / 2, db * 16 + hh * 8);
-        ts[db] = load_tab8(p.sin_tab, tab_row, D / 2, db * 16 + hh * 8);
+        for (int db = 0; db < NDB / 2; ++db) {
+          const int c0 = db * 4 + hh * 2;
+          const floatx4 c_lo = *reinterpret_cast<const floatx4*>(smem + 3 * TB + pr * Tl::ROW_BYTES + Tl::k_chunk(pr, c0) * 16);
+          const floatx4 c_hi = *reinterpret_cast<const floatx4*>(smem + 3 * TB + pr * Tl::ROW_BYTES + Tl::k_chunk(pr, c0 + 1) * 16);
+          const floatx4 s_lo = *reinterpret_cast<const floatx4*>(smem + 4 * TB + pr * Tl::ROW_BYTES + Tl::k_chunk(pr, c0) * 16);
+          const floatx4 s_hi = *reinterpret_cast<const floatx4*>(smem + 4 * TB + pr * Tl::ROW_BYTES + Tl::k_chunk(pr, c0 + 1) * 16);
+          tc[db] = floatx8{c_lo[0], c_lo[1], c_lo[2], c_lo[3], c_hi[0], c_hi[1], c_hi[2], c_hi[3]} + bad;
+          ts[db] = floatx8{s_lo[0], s_lo[1], s_lo[2], s_lo[3], s_hi[0], s_hi[1], s_hi[2], s_hi[3]} + bad;
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB / 2; ++db) {
+          tc[db] = load_tab8(p.cos_tab, tab_row, D / 2, db * 16 + hh * 8);
+          ts[db] = load_tab8(p.sin_tab, tab_row, D / 2, db * 16 + hh * 8);
+        }
       }
     }
   }
