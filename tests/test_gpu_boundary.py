@@ -285,6 +285,32 @@ def test_out_of_range_device_positions_give_nan_rows():
     assert torch.isnan(dec).all()
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(2, 2), (8, 2)])
+def test_pos_base_past_the_tables_gives_nan_rows(Hq, Hkv):
+    """Per-sequence position bases (device tensor) run the prefill's staged cos/sin rows:
+    the rows whose position lies past the tables are NaN, every other row matches the
+    oracle at its own position."""
+    say(f"prefill pos_base past the tables {Hq}/{Hkv}")
+    B, S, D, max_pos = 2, 8, 64, 16
+    cos, sin = rope_tables(D, max_pos, 1e6)
+    q = randn(B, Hq, S, D, seed=3321, dtype=torch.bfloat16)
+    k = randn(B, Hkv, S, D, seed=3322, dtype=torch.bfloat16)
+    v = randn(B, Hkv, S, D, seed=3323, dtype=torch.bfloat16)
+    w = torch.ones(D)
+    base = torch.tensor([3, max_pos - 4], dtype=torch.int32)
+    o = nq.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), q_weight=w.to(DEV), eps=1e-6, cos=cos.to(DEV),
+                             sin=sin.to(DEV), pos_base=base.to(DEV), causal=True).float().cpu()
+    assert torch.isnan(o[1, :, 4:]).all() and torch.isfinite(o[1, :, :4]).all() and torch.isfinite(o[0]).all()
+    from oracle import rms_norm, rotate_half
+    for bi in range(B):
+        pos = torch.arange(S) + int(base[bi])
+        ok = pos < max_pos
+        qh = rms_norm(q[bi:bi + 1].float(), w, 1e-6)
+        qh = rotate_half(qh, cos[pos.clamp(max=max_pos - 1)][None, None], sin[pos.clamp(max=max_pos - 1)][None, None])
+        ref = attention(qh, k[bi:bi + 1].float(), v[bi:bi + 1].float(), causal=True)[0]
+        assert_bf16_close(o[bi][:, ok], ref[:, ok], f"pos_base row {bi}")
+
+
 # ------------------------------------------------------------------ RMSNorm mirror
 
 @pytest.mark.parametrize("width", [32, 128, 256, 2048])
