@@ -36,6 +36,8 @@
 //
 // The cache is read exactly once: HBM-bound at 16 FLOP/byte for G = 16.
 
+#include <type_traits>
+
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
 #include "nq_prefill.hpp"
@@ -130,15 +132,6 @@ template <> struct Piece<bf16> {
   }
   __device__ __forceinline__ static bf16x8 to_bf16(type v) { return v; }
 };
-template <> struct Piece<float> {
-  typedef floatx8 type;
-  __device__ __forceinline__ static type load(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    floatx4 a = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, DC_AUX_NT));
-    floatx4 b = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, DC_AUX_NT));
-    return floatx8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  }
-  __device__ __forceinline__ static bf16x8 to_bf16(type v) { return __builtin_convertvector(v, bf16x8); }
-};
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -212,9 +205,11 @@ __device__ __forceinline__ int64_t wave_begin(const DecodeParams& p, int64_t N, 
   return p.span > 0 ? min(N, w * p.span) : w * N / We;
 }
 // ---------------------------------------------------------------- kernels
-template <int D, typename T, bool PIPE, bool PAGED, bool APPEND>
+// bf16 caches (fp32 caches run the fp32 prefill kernel at S = 1)
+template <int D, typename T, bool PAGED, bool APPEND>
 __global__ void __attribute__((amdgpu_flat_work_group_size(DC_THREADS, DC_THREADS), amdgpu_waves_per_eu(DC_WG_PER_CU)))
 decode_stream_kernel(DecodeParams p) {
+  static_assert(std::is_same<T, bf16>::value, "bf16 cache");
   using L = DcTile<D>;
   using P8 = Piece<T>;
   constexpr int NDQ = D / 32;  // 32-wide d blocks (QK^T k-steps)
@@ -472,7 +467,7 @@ decode_stream_kernel(DecodeParams p) {
         *reinterpret_cast<bf16x8*>(vt + rr * L::RB + ((sub ^ L::vswz(rr)) << 4)) = to_bf16x8(va1);
         *reinterpret_cast<bf16x8*>(vt + rr * L::RB + ((c2 ^ L::vswz(rr)) << 4)) = to_bf16x8(va2);
       }
-      if (PIPE && s + 1 < nseg) load(k0 + DC_STEP);
+      if (s + 1 < nseg) load(k0 + DC_STEP);
 
       floatx4 sc[2];
 #pragma unroll
@@ -522,7 +517,6 @@ decode_stream_kernel(DecodeParams p) {
                                       reinterpret_cast<const bf16*>(src + 16 * L::RB));
         oacc[dd] = mfma16(a, pop, oacc[dd]);
       }
-      if (!PIPE && s + 1 < nseg) load(k0 + DC_STEP);
     }
 
     // ---- flush the segment
@@ -640,7 +634,7 @@ static int64_t dc_workspace(int B, int Hq, int Hkv, int D, int max_len, int chun
 
 template <int D, typename T, bool PAGED, bool APPEND>
 static hipError_t launch_decode(DecodeParams p, hipStream_t st) {
-  auto kern = decode_stream_kernel<D, T, sizeof(T) == 2, PAGED, APPEND>;
+  auto kern = decode_stream_kernel<D, T, PAGED, APPEND>;
   if (p.span == 0) {
     // persistent grid: as many waves as stay resident at once (<= DC_MAX_WAVES),
     // worked out once per device and kernel variant
