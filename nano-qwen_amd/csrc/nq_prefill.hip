@@ -85,6 +85,17 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 
+// This lane's index (0..63), computed afresh (volatile, so the compiler cannot
+// reuse an earlier value): code after the main loop derives its lane-dependent
+// values from it instead of keeping them live through the loop, where they
+// would be spilled and reloaded (and a reload, counted by vmcnt like the tile
+// loads in flight, waits for those loads too).
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // MFMA row r of a 32-key block holds key sigma(r): bits 2 and 3 swapped.
 __device__ __forceinline__ int key_perm32(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
@@ -327,6 +338,9 @@ prefill_kernel(PrefillParams p) {
 
   // ---- per-lane LDS read offsets (bytes within a tile)
   // K: MFMA row sigma(r32) (+32 for the second key block), chunk 2*db + hh
+  static_assert(Tl::CPR * 16 == Tl::ROW_BYTES && NDB * 2 <= Tl::CPR && NDO * 4 <= Tl::CPR,
+                "k_off[db] == k_off[0] ^ (db << 5), v_off[dd] == v_off[0] ^ (dd << 6): "
+                "the swizzled chunk bits stay below the row bits");
   int k_off[NDB];
   {
     const int row = key_perm32(r32);
@@ -364,12 +378,26 @@ prefill_kernel(PrefillParams p) {
   // (one extra MFMA per 32-key block, k-slots 0 and 1) + K Q^T.  Every score
   // then leaves the MFMA already offset by the row max, and exp2 takes it as is.
   float m_i = 0.f, l_i = 0.f;
-  bf16x8 ones_op, qaug;
+  bf16x8 qaug;
+  // [1 1 0 ..] in the lanes of k-slots 0..7 (hh = 0), zeros in the others.
+  // 4-wave workgroups build it where it is used, from a fresh lane index:
+  // held through the loop, it is what their register allocation spills (and
+  // reloads every step); 8-wave workgroups keep it in registers.
+  bf16x8 ones_held;
   {
     const bf16 one = hh == 0 ? (bf16)1.0f : (bf16)0.0f;
     const bf16 z = (bf16)0.0f;
-    ones_op = bf16x8{one, one, z, z, z, z, z, z};
+    ones_held = bf16x8{one, one, z, z, z, z, z, z};
   }
+  auto ones_op = [&]() {
+    if constexpr (NW == 4) {
+      const bf16 one = (fresh_lane() >> 5) == 0 ? (bf16)1.0f : (bf16)0.0f;
+      const bf16 z = (bf16)0.0f;
+      return bf16x8{one, one, z, z, z, z, z, z};
+    } else {
+      return ones_held;
+    }
+  };
   // m_i <- m rounded to the nearest hi + lo bf16 pair; qaug <- (-hi, -lo)
   auto set_max = [&](float m) {
     const bf16 mh = (bf16)m;
@@ -392,14 +420,20 @@ prefill_kernel(PrefillParams p) {
   qk(0, sA[0], sA[1]);
 
   // masking of tile n0: keys past T, and (causal) keys past this row's frontier
+  // 1/G as a wave-uniform float: (R + 0.5) / G rounds down to R / G exactly
+  // for R < 2^16, without the integer-division sequence and its constants
+  const float inv_g = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, 1.0f / (float)p.G)));
   auto mask_tile = [&](floatx16* s, int n0) {
     if ((n0 + PF_BN > Tk) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff)) {
-      const int lim = CAUSAL ? min(Tk - 1, qi + coff) : Tk - 1;
+      const int ml = fresh_lane();
+      const int mhh = ml >> 5;
+      const int mqi = q0 + (int)(((float)(wave * 32 + (ml & 31)) + 0.5f) * inv_g);
+      const int lim = CAUSAL ? min(Tk - 1, mqi + coff) : Tk - 1;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int key = n0 + kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
+          const int key = n0 + kb * 32 + (i >> 3) * 16 + mhh * 8 + (i & 7);
           if (key > lim) s[kb][i] = -INFINITY;
         }
     }
@@ -484,10 +518,17 @@ prefill_kernel(PrefillParams p) {
     auto issue = [&](auto I) {
       constexpr int i = decltype(I)::value;
       if constexpr (i < NQK) {
-        opnd[i % (PD + 1)] = lds_read_b128_nowait<(i % 2) * 32 * Tl::ROW_BYTES>(Kt + k_off[i / 2]);
+        // k_off[db] = k_off[0] ^ (db << 5) (the XOR swizzle moves the chunk
+        // index, whose bits sit below the row's).  The masked steps, which come
+        // last, derive it so the other seven offsets die after the unmasked
+        // loop instead of being spilled and reloaded around the masked steps.
+        const uint32_t ko = MASKN ? (uint32_t)(k_off[0] ^ ((i / 2) << 5)) : (uint32_t)k_off[i / 2];
+        opnd[i % (PD + 1)] = lds_read_b128_nowait<(i % 2) * 32 * Tl::ROW_BYTES>(Kt + ko);
       } else {
         constexpr int t = i - NQK;
-        opnd[i % (PD + 1)] = lds_read_tr8_nowait<8 * D>(Vt + v_off[t % NDO] + (t / NDO) * 16 * Tl::ROW_BYTES);
+        // likewise v_off[dd] = v_off[0] ^ (dd << 6)
+        const uint32_t vo = MASKN ? (uint32_t)(v_off[0] ^ ((t % NDO) << 6)) : (uint32_t)v_off[t % NDO];
+        opnd[i % (PD + 1)] = lds_read_tr8_nowait<8 * D>(Vt + vo + (t / NDO) * 16 * Tl::ROW_BYTES);
       }
     };
     // P[j] values e: exp2, and per 8 values a bf16 pack and its row sum
@@ -500,7 +541,7 @@ prefill_kernel(PrefillParams p) {
     };
     static_for<0, (PD < NOPS ? PD : NOPS)>(issue);
     floatx16 s_init;  // -m_i in every element; the first MFMA of each key half starts from it
-    if (NEXT) s_init = mfma32(ones_op, qaug, floatx16{});
+    if (NEXT) s_init = mfma32(ones_op(), qaug, floatx16{});
     if (NQK == 0) {  // last tile: all of P[j] before the PV stream
 #pragma unroll
       for (int e = 0; e < 32; ++e) pwork(e);
@@ -575,20 +616,21 @@ prefill_kernel(PrefillParams p) {
   static_assert(32 * NW * Tl::ROW_BYTES <= 4 * TB, "output stage fits the tile buffers");
   __syncthreads();  // every wave is done with the last K/V tiles
   unsigned char* const ostage = smem + wave * 32 * Tl::ROW_BYTES;
+  const int el = fresh_lane(), er32 = el & 31, ehh = el >> 5;
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const floatx4 t = {oacc[dd][gq * 4 + 0] * inv_l, oacc[dd][gq * 4 + 1] * inv_l,
                          oacc[dd][gq * 4 + 2] * inv_l, oacc[dd][gq * 4 + 3] * inv_l};
-      *reinterpret_cast<bf16x4*>(ostage + r32 * Tl::ROW_BYTES + Tl::k_chunk(r32, dd * 4 + gq) * 16 + hh * 8) =
+      *reinterpret_cast<bf16x4*>(ostage + er32 * Tl::ROW_BYTES + Tl::k_chunk(er32, dd * 4 + gq) * 16 + ehh * 8) =
           __builtin_convertvector(t, bf16x4);
     }
   {
     constexpr int RPR = 64 / OCH;  // rows per read-back instruction
 #pragma unroll
     for (int i = 0; i < 32 / RPR; ++i) {
-      const int r = i * RPR + lane / OCH, c = lane % OCH;
+      const int r = i * RPR + el / OCH, c = el % OCH;
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(ostage + r * Tl::ROW_BYTES + Tl::k_chunk(r, c) * 16);
       const int Rw = wave * 32 + r;
       const int qr = q0 + Rw / p.G;
@@ -597,7 +639,11 @@ prefill_kernel(PrefillParams p) {
                                    (int64_t)qr * p.oss + c * 8) = v;
     }
   }
-  if (p.lse && hh == 0 && qvalid) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = (m_i + __log2f(l_i)) * kLn2;
+  if (p.lse && ehh == 0) {
+    const int eR = wave * 32 + er32;
+    const int eq = q0 + eR / p.G;
+    if (eq < p.S) p.lse[((int64_t)b * p.Hq + kvh * p.G + eR % p.G) * p.S + eq] = (m_i + __log2f(l_i)) * kLn2;
+  }
 }
 
 template <int D, typename T, int NW>
