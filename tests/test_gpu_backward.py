@@ -62,6 +62,28 @@ def test_attention_backward_against_fp64_autograd(D, Hq, Hkv, causal):
     _close_rel(dv, rv, "dv")
 
 
+@pytest.mark.parametrize("S,T,Hq,Hkv,causal", [
+    (2, 2, 2, 2, True), (17, 17, 2, 2, True), (32, 32, 2, 2, True), (33, 33, 2, 2, True),
+    (64, 64, 2, 2, True), (96, 96, 2, 2, True), (129, 129, 2, 1, True), (250, 250, 4, 1, True),
+    (40, 300, 2, 1, True), (96, 96, 2, 2, False), (33, 200, 4, 2, False)])
+def test_dkdv_steps_per_block_and_partial_tiles(S, T, Hq, Hkv, causal):
+    """head_dim 128: key blocks that walk one, two, three or many query steps, a top
+    tile that runs past S, keys past the last query (bottom-right causal) and keys
+    of a block past T (every wave of the dK/dV kernel masked or partly masked)."""
+    say(f"bwd steps S={S} T={T} {Hq}/{Hkv} causal={causal}")
+    B, D = 2, 128
+    q = randn(B, Hq, S, D, seed=531, dtype=torch.bfloat16)
+    k = randn(B, Hkv, T, D, seed=532, dtype=torch.bfloat16)
+    v = randn(B, Hkv, T, D, seed=533, dtype=torch.bfloat16)
+    do = randn(B, Hq, S, D, seed=534, dtype=torch.bfloat16)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=causal)
+    _, rq, rk, rv = _ref_grads(q, k, v, do, causal)
+    _close_rel(dq, rq, "dq")
+    _close_rel(dk, rk, "dk")
+    _close_rel(dv, rv, "dv")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_attention_backward_bottom_right_causal_and_dtypes(dtype):
     """S < T (queries are the last S positions), ragged sizes, fp32 storage too."""
