@@ -97,6 +97,38 @@ __device__ __forceinline__ void bw_tile(unsigned char* tile, const T* src, int64
   }
 }
 
+// The same staging of a full bf16 tile (all NR rows valid) with buffer loads:
+// the tile in a scalar descriptor, the lane's offset in one VGPR and each
+// instruction's row step as a scalar offset.  Instruction m = wave + NW*i
+// covers rows 4m.. (D = 128; 1024 / (2D) rows per instruction in general):
+// the lane's row moves by a multiple of the swizzle period with i, so its
+// chunk, and hence its offset, is the same for every i.
+template <int D, int NR, bool TSW, int NW = 4>
+__device__ __forceinline__ void bw_tile_full(unsigned char* tile, const bf16* src, int64_t rs, int wave,
+                                             int lane) {
+  using L = BwTile<D>;
+  constexpr int NI = NR * L::RB / 1024;
+  constexpr int RPI = 1024 / L::RB;
+  static_assert(NI % NW == 0 || NI < NW, "tile size");
+  if (NI < NW && wave >= NI) return;
+  const int r0 = (wave * 1024 + lane * 16) / L::RB, pc = (lane * 16 % L::RB) / 16;
+  const int lc = TSW ? L::tsw(r0, pc) : L::rsw(r0, pc);
+  const uint32_t rb = (uint32_t)(rs * 2);
+  const BufRsrc r = make_rsrc(src, NR * rb);
+  const uint32_t off = r0 * rb + lc * 16;
+#pragma unroll
+  for (int i = 0; i < (NI < NW ? 1 : NI / NW); ++i)
+    buffer_load_lds16(r, tile + (wave + NW * i) * 1024, off, i * NW * RPI * rb);
+}
+
+// The lane id, computed where it is used (opaque to the compiler, so not
+// hoisted into a register held across a loop).
+__device__ __forceinline__ int bw_fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Transpose-read operand: rows r0..r0+3 at `addr`, r0+4..r0+7 four rows on.
 template <int D>
 __device__ __forceinline__ bf16x8 bw_tr8(const unsigned char* p) {
@@ -140,6 +172,13 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
   const T* vb0 = reinterpret_cast<const T*>(p.v) + b * p.vsb + kvh * p.vsh;
   auto stage = [&](int j, int buf) {
     const int n0 = j * BW_BN;
+    if (sizeof(T) == 2 && n0 + BW_BN <= Tk) {
+      bw_tile_full<D, BW_BN, true, NW>(smem + buf * 2 * TB, reinterpret_cast<const bf16*>(kb0 + (int64_t)n0 * p.kss),
+                                       p.kss, wave, lane);
+      bw_tile_full<D, BW_BN, false, NW>(smem + buf * 2 * TB + TB,
+                                        reinterpret_cast<const bf16*>(vb0 + (int64_t)n0 * p.vss), p.vss, wave, lane);
+      return;
+    }
     // rows past the sequence's keys clamp to its last key (masked; padding
     // rows are never read)
     bw_tile<D, T, BW_BN, true, NW>(smem + buf * 2 * TB, kb0 + (int64_t)n0 * p.kss, p.kss, Tk - n0, wave, lane);
@@ -362,16 +401,24 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   constexpr int NPW = NI >= 4 ? NI / 4 : 1;
   constexpr int DSTEP = 4 * 1024 / L::RB;
   static_assert(NI % 4 == 0 || NI < 4, "tile size");
-  const int dr0 = (wave * 1024 + lane * 16) / L::RB;
-  const int dlc = L::tsw(dr0, (lane * 16 % L::RB) / 16) * 8;
   // stage the (head g, query tile qt) step into buffer buf
   auto stage = [&](int g, int qt, int buf) {
     const int head = kvh * p.G + g;
     unsigned char* base = smem + buf * BUF;
     const T* qsrc = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qt * p.qss;
     const T* dsrc = reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qt * p.doss;
-    if constexpr (sizeof(T) == 2) {
-      const int last = p.S - qt - 1;  // rows past S clamp to the last row (masked)
+    if (sizeof(T) == 2 && qt + BW_BQ <= p.S) {
+      bw_tile_full<D, BW_BQ, true>(base, reinterpret_cast<const bf16*>(qsrc), p.qss, wave, lane);
+      bw_tile_full<D, BW_BQ, true>(base + TB, reinterpret_cast<const bf16*>(dsrc), p.doss, wave, lane);
+    } else if constexpr (sizeof(T) == 2) {
+      // the top tile of a sequence whose length is not a multiple of 32 (rows
+      // past S clamp to the last row; they are masked).  The lane's row and
+      // chunk come from a fresh lane id: held across the loop they would take
+      // a register that the loop then spills.
+      const int fl = bw_fresh_lane();
+      const int dr0 = (wave * 1024 + fl * 16) / L::RB;
+      const int dlc = L::tsw(dr0, (fl * 16 % L::RB) / 16) * 8;
+      const int last = p.S - qt - 1;
 #pragma unroll
       for (int i = 0; i < NPW; ++i) {
         if (NI < 4 && wave >= NI) break;
