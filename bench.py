@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 GQA attention hot path (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads ...]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-s T] [--workloads ...]
 
 A step is one pass of the attention hot path over one batch of synthetic,
 seeded inputs already resident in HBM:
@@ -13,9 +13,15 @@ The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 (B8 S2048 Hq16 Hkv8 D128 causal bf16); FLOPs are the algorithmic
 4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
 prefill kernel's own FLOPs by its average duration from HIP events recorded
-on its launch stream.  ``secondary`` holds the other workloads, each with its
+on its launch stream, in a second pass over the same steps (``ms_per_step``
+comes from a pass with no events between the launches).  ``secondary`` holds the other workloads, each with its
 roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs
 2.5x the forward's, the five matrix products of FlashAttention-2).
+Before its W warmup and K timed steps, each workload runs its own step
+untimed for ``--settle-s`` seconds (default 0.2): the GPU raises its clock over
+the first ~40 ms of sustained load (the 1.7B-like step goes from ~0.20 to
+~0.165 ms) and lowers it again after ~0.5 s idle, e.g. while a CPU baseline
+runs, so without it the short workloads would be timed during the ramp.
 ``cpu_baseline`` (top level for the headline, inside each ``secondary`` entry
 for the others) times the reference's own composition -- QK-Norm, RoPE,
 repeat_interleave, SDPA, restated in the oracle -- in fp32 on the host cores, on
@@ -274,18 +280,44 @@ def measured_traffic():
     return {w: int(b) for w, b in out.items()}
 
 
+def settle(w, seconds):
+    """Untimed back-to-back steps for `seconds` (at least one): the GPU raises
+    its clock over the first ~40 ms of sustained load and drops it again when
+    idle, so a workload's W warmup and K timed steps follow its own settle."""
+    t0 = time.perf_counter()
+    w.step()
+    torch.cuda.synchronize()
+    first = time.perf_counter() - t0
+    every = max(1, int(0.01 / max(first, 1e-6)))  # check the clock about every 10 ms
+    n = 1
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(every):
+            w.step()
+        n += every
+        torch.cuda.synchronize()
+    return n
+
+
 def time_workload(w, steps, warmup):
+    """Step time from `steps` back-to-back steps with nothing between their
+    launches; then the same steps again with HIP events around the timed kernel
+    on its launch stream, for its average duration.  (An event recorded between
+    two launches holds the next dispatch ~6 us on this GPU, so the step time is
+    not taken from the pass that carries them.)"""
     for _ in range(warmup):
         w.step()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        w.step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         w.step(evs[i])
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
     kernel_ms = sorted(a.elapsed_time(b) for a, b in evs)
     avg_kernel = sum(kernel_ms) / len(kernel_ms)
     return wall_ms / steps, avg_kernel, kernel_ms[len(kernel_ms) // 2]
@@ -449,6 +481,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-s", type=float, default=0.2,
+                    help="untimed steps for this long before each workload's warmup (GPU clock ramp)")
     ap.add_argument("--workloads", default="c2,c3,c4,c4_paged,c5,c2_bwd,c3_bwd",
                     help="comma list of c2 (headline), c3, c4, c4_paged, c5, c2_bwd, c3_bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -507,11 +541,14 @@ def main():
         # C5 takes ~0.1 s a step: at least 5 timed steps, a bounded number
         steps = args.steps if name != "c5" else max(5, min(args.steps, 8))
         warm = args.warmup if name != "c5" else 1
-        log(f"{name}: {steps} timed steps after {warm} warmup")
+        n_settle = settle(w, args.settle_s)
+        log(f"{name}: {steps} timed steps after {warm} warmup ({n_settle} settle steps, "
+            f"{args.settle_s} s)")
         step_ms, kern_ms, kern_med = time_workload(w, steps, warm)
         val, unit = w.throughput(step_ms)
         results[name] = {"config": w.describe(), "value": round(val, 3), "unit": unit,
                          "ms_per_step": round(step_ms, 5), "steps": steps, "warmup": warm,
+                         "settle_steps": n_settle,
                          "roofline": w.roofline(kern_ms)}
         log(f"{name}: {step_ms:.4f} ms/step, kernel avg {kern_ms:.4f} ms, {val:.2f} {unit}")
         if not args.no_cpu_baseline:
@@ -535,6 +572,7 @@ def main():
     line = {
         "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1,
         "steps": head["steps"], "warmup": head["warmup"], "ms_per_step": head["ms_per_step"],
+        "settle_s": args.settle_s, "settle_steps": head["settle_steps"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) inputs, QK-Norm weights 1+0.02*N(0,1))",
         "config": head["config"], "roofline": head["roofline"],
