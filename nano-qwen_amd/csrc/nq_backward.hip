@@ -121,14 +121,6 @@ __device__ __forceinline__ void bw_tile_full(unsigned char* tile, const bf16* sr
     buffer_load_lds16(r, tile + (wave + NW * i) * 1024, off, i * NW * RPI * rb);
 }
 
-// The lane id, computed where it is used (opaque to the compiler, so not
-// hoisted into a register held across a loop).
-__device__ __forceinline__ int bw_fresh_lane() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
-
 // Transpose-read operand: rows r0..r0+3 at `addr`, r0+4..r0+7 four rows on.
 template <int D>
 __device__ __forceinline__ bf16x8 bw_tr8(const unsigned char* p) {
@@ -401,24 +393,19 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   constexpr int NPW = NI >= 4 ? NI / 4 : 1;
   constexpr int DSTEP = 4 * 1024 / L::RB;
   static_assert(NI % 4 == 0 || NI < 4, "tile size");
+  const int dr0 = (wave * 1024 + lane * 16) / L::RB;
+  const int dlc = L::tsw(dr0, (lane * 16 % L::RB) / 16) * 8;
   // stage the (head g, query tile qt) step into buffer buf
   auto stage = [&](int g, int qt, int buf) {
     const int head = kvh * p.G + g;
     unsigned char* base = smem + buf * BUF;
     const T* qsrc = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qt * p.qss;
     const T* dsrc = reinterpret_cast<const T*>(p.dout) + b * p.dosb + head * p.dosh + (int64_t)qt * p.doss;
-    if (sizeof(T) == 2 && qt + BW_BQ <= p.S) {
-      bw_tile_full<D, BW_BQ, true>(base, reinterpret_cast<const bf16*>(qsrc), p.qss, wave, lane);
-      bw_tile_full<D, BW_BQ, true>(base + TB, reinterpret_cast<const bf16*>(dsrc), p.doss, wave, lane);
-    } else if constexpr (sizeof(T) == 2) {
-      // the top tile of a sequence whose length is not a multiple of 32 (rows
-      // past S clamp to the last row; they are masked).  The lane's row and
-      // chunk come from a fresh lane id: held across the loop they would take
-      // a register that the loop then spills.
-      const int fl = bw_fresh_lane();
-      const int dr0 = (wave * 1024 + fl * 16) / L::RB;
-      const int dlc = L::tsw(dr0, (fl * 16 % L::RB) / 16) * 8;
-      const int last = p.S - qt - 1;
+    if constexpr (sizeof(T) == 2) {
+      // (per-instruction addresses even for full tiles: the buffer-descriptor
+      // form of the dQ kernel raised this kernel's HBM fetch at the 8B-like
+      // shape from 3.65 to 5.45 GB per launch, at equal time)
+      const int last = p.S - qt - 1;  // rows past S clamp to the last row (masked)
 #pragma unroll
       for (int i = 0; i < NPW; ++i) {
         if (NI < 4 && wave >= NI) break;
