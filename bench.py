@@ -12,10 +12,10 @@ seeded inputs already resident in HBM:
 The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 (B8 S2048 Hq16 Hkv8 D128 causal bf16); FLOPs are the algorithmic
 4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
-prefill kernel's own FLOPs by its average duration from HIP events recorded
-on its launch stream, in a second pass over the same steps (``ms_per_step``
-comes from a pass with no events between the launches).  ``secondary`` holds the other workloads, each with its
-roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs
+prefill kernel's own FLOPs by its average duration: K launches of it back to
+back on its launch stream between two HIP events, after the K timed steps
+(``ms_per_step``, with nothing between the launches).  ``secondary`` holds
+the other workloads, each with its roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs
 2.5x the forward's, the five matrix products of FlashAttention-2).
 Before its W warmup and K timed steps, each workload runs its own step
 untimed for ``--settle-s`` seconds (default 0.2): the GPU raises its clock over
@@ -93,13 +93,13 @@ class Prefill:
                                            cos=self.cos, sin=self.sin, causal=True, out=self.out,
                                            plan=True)
 
-    def step(self, ev=None):
+    def step(self):
         self.k_call.launch()
-        if ev is not None:
-            ev[0].record()
         self.p_call.launch()
-        if ev is not None:
-            ev[1].record()
+
+    def timed_launch(self):
+        """The kernel the roofline is about (K-hat is unchanged between steps)."""
+        self.p_call.launch()
 
     def describe(self):
         return {"workload": self.name, "batch": self.B, "seq_len": self.S, "num_heads": self.Hq,
@@ -148,13 +148,13 @@ class Decode:
                                           q_weight=self.w, eps=1e-6, cos=self.cos, sin=self.sin,
                                           out=self.out, workspace=self.ws, plan=True)
 
-    def step(self, ev=None):
+    def step(self):
         self.a_call.launch()
-        if ev is not None:
-            ev[0].record()
         self.d_call.launch()
-        if ev is not None:
-            ev[1].record()
+
+    def timed_launch(self):
+        """The decode kernel and its merge (the append writes the same rows every step)."""
+        self.d_call.launch()
 
     def describe(self):
         return {"workload": self.name, "batch": self.B, "num_heads": self.Hq,
@@ -207,12 +207,11 @@ class PagedDecode(Decode):
             v_new=self.vnew, k_weight=self.w, lens_out=self.lens_out, q_weight=self.w, eps=1e-6,
             cos=self.cos, sin=self.sin, out=self.out, workspace=self.ws, plan=True)
 
-    def step(self, ev=None):
-        if ev is not None:
-            ev[0].record()
+    def step(self):
         self.d_call.launch()
-        if ev is not None:
-            ev[1].record()
+
+    def timed_launch(self):
+        self.d_call.launch()
 
     def describe(self):
         d = super().describe()
@@ -238,12 +237,11 @@ class Backward:
         self.call = nq.ops.attention_backward(self.q, self.k, self.v, self.o, self.do, self.lse,
                                               causal=True, plan=True)
 
-    def step(self, ev=None):
-        if ev is not None:
-            ev[0].record()
+    def step(self):
         self.call.launch()
-        if ev is not None:
-            ev[1].record()
+
+    def timed_launch(self):
+        self.call.launch()
 
     def describe(self):
         return {"workload": self.name, "batch": self.B, "seq_len": self.S, "num_heads": self.Hq,
@@ -300,10 +298,11 @@ def settle(w, seconds):
 
 def time_workload(w, steps, warmup):
     """Step time from `steps` back-to-back steps with nothing between their
-    launches; then the same steps again with HIP events around the timed kernel
-    on its launch stream, for its average duration.  (An event recorded between
-    two launches holds the next dispatch ~6 us on this GPU, so the step time is
-    not taken from the pass that carries them.)"""
+    launches; then the timed kernel(s) alone, `steps` launches back to back on
+    their launch stream between two HIP events, for their average duration.
+    (An event recorded between two launches holds the next dispatch ~6 us on
+    this GPU and lengthens the bracketed interval, so neither figure is taken
+    with events between launches.)"""
     for _ in range(warmup):
         w.step()
     torch.cuda.synchronize()
@@ -312,15 +311,14 @@ def time_workload(w, steps, warmup):
         w.step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    for i in range(steps):
-        w.step(evs[i])
+    start.record()
+    for _ in range(steps):
+        w.timed_launch()
+    end.record()
     torch.cuda.synchronize()
-    kernel_ms = sorted(a.elapsed_time(b) for a, b in evs)
-    avg_kernel = sum(kernel_ms) / len(kernel_ms)
-    return wall_ms / steps, avg_kernel, kernel_ms[len(kernel_ms) // 2]
+    return wall_ms / steps, start.elapsed_time(end) / steps
 
 
 def _host():
@@ -544,7 +542,7 @@ def main():
         n_settle = settle(w, args.settle_s)
         log(f"{name}: {steps} timed steps after {warm} warmup ({n_settle} settle steps, "
             f"{args.settle_s} s)")
-        step_ms, kern_ms, kern_med = time_workload(w, steps, warm)
+        step_ms, kern_ms = time_workload(w, steps, warm)
         val, unit = w.throughput(step_ms)
         results[name] = {"config": w.describe(), "value": round(val, 3), "unit": unit,
                          "ms_per_step": round(step_ms, 5), "steps": steps, "warmup": warm,
