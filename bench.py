@@ -15,8 +15,9 @@ The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 prefill kernel's own FLOPs by its average duration: K launches of it back to
 back on its launch stream between two HIP events, after the K timed steps
 (``ms_per_step``, with nothing between the launches).  ``secondary`` holds
-the other workloads, each with its roofline (decode bytes = sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs
-2.5x the forward's, the five matrix products of FlashAttention-2).
+the other workloads, each with its roofline (decode bytes
+sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs 2.5x the forward's, the five
+matrix products of FlashAttention-2).
 Before its W warmup and K timed steps, each workload runs its own step
 untimed for ``--settle-s`` seconds (default 0.2): the GPU raises its clock over
 the first ~40 ms of sustained load (the 1.7B-like step goes from ~0.20 to
