@@ -240,7 +240,7 @@ prefill_kernel(PrefillParams p) {
   load_v(0, 0);
   if (ntiles > 1) load_k(1, 1);
   if (stage_tab) {
-    const int pos0 = (p.q_pos_base ? p.q_pos_base[b] : p.q_pos0) + q0;
+    const int pos0 = (p.q_pos_base ? ld_uniform(p.q_pos_base, b) : p.q_pos0) + q0;
     constexpr int TROW = D * 2;  // bytes per table row
     const int ninst = (p.BM * TROW + 1023) / 1024;
     for (int m = wave; m < ninst; m += NW) {
@@ -253,16 +253,11 @@ prefill_kernel(PrefillParams p) {
     }
   }
   floatx8 xf[NDB];
-  floatx8 wq[NDB];
   floatx8 tc[NDB / 2], ts[NDB / 2];
   {
     const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + head * p.qsh + (int64_t)qi_c * p.qss;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) xf[db] = Vec8<T>::load_f32(qrow + db * 16 + hh * 8);
-    if (do_norm) {
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) wq[db] = Vec8<float>::load_f32(p.qw + db * 16 + hh * 8);
-    }
     if (do_rope) {
       if (stage_tab) {
         wait_vmcnt0();
@@ -301,10 +296,18 @@ prefill_kernel(PrefillParams p) {
         for (int e = 0; e < 8; ++e) ss += xf[db][e] * xf[db][e];
       ss = xor32_sum(ss);
       const float r = rsqrtf(ss / (float)D + p.eps);
+      // the weights through the scalar path: the 32 lanes of a half-wave need
+      // the same 8, so both halves' values come as wave-uniform loads and each
+      // lane selects its own (as vector loads, 16 of them issued at ~220
+      // clocks each: 1.8 us of a ~7.5 us prologue at the 1.7B-like shape)
+      const auto* wc = (const __attribute__((address_space(4))) float*)p.qw;  // read-only
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xf[db][e] = xf[db][e] * r * wq[db][e];
+        for (int e = 0; e < 8; ++e) {
+          const float w0 = wc[db * 16 + e], w1 = wc[db * 16 + 8 + e];
+          xf[db][e] = xf[db][e] * r * (hh ? w1 : w0);
+        }
     }
     if (do_rope) {
 #pragma unroll

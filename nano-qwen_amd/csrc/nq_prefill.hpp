@@ -44,7 +44,7 @@ struct PrefillParams {
 // Keys of sequence b (-1: a length out of range).
 __device__ __forceinline__ int pf_keys(const PrefillParams& p, int b) {
   if (!p.kv_lens) return p.T;
-  const int l = p.kv_lens[b];
+  const int l = ld_uniform(p.kv_lens, b);
   return (l < 0 || l > p.kv_max - p.kv_extra) ? -1 : l + p.kv_extra;
 }
 
