@@ -290,3 +290,37 @@ def test_wide_workgroups(D, Hq, Hkv, B, S):
     for b, kvh in ((0, 0), (B - 1, Hkv - 1)):
         for (r0, r1), ref in zip(rows, _sampled_blocks(q, k, v, qw, kw, cos, sin, b, kvh, G, rows)):
             assert_bf16_close(o[b:b + 1, kvh * G:(kvh + 1) * G, r0:r1], ref, f"wide b={b} kvh={kvh} rows={r0}")
+
+
+def test_staged_tables_match_per_token_positions_at_8_waves():
+    """At an 8-wave shape (>= 2048 workgroups of 64 positions x 4 heads), the cos/sin rows
+    staged in LDS for per-sequence position bases, or for a uniform offset, give the same
+    output bits as explicit per-token positions (per-lane table loads): same table
+    entries, same arithmetic.  Key lengths (read through the scalar path) are exercised
+    alongside: a padded batch row gives the same bits either way too."""
+    say("prefill staged tables vs per-token positions, 8 waves")
+    B, S, Hq, Hkv, D = 8, 4096, 16, 4, 128
+    cos, sin = rope_tables(D, S + 64, 1e6)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    q = torch.randn(B, S, Hq, D, device=DEV, generator=torch.Generator(DEV).manual_seed(41),
+                    dtype=torch.bfloat16).transpose(1, 2)
+    k = torch.randn(B, S, Hkv, D, device=DEV, generator=torch.Generator(DEV).manual_seed(42),
+                    dtype=torch.bfloat16).transpose(1, 2)
+    v = torch.randn(B, S, Hkv, D, device=DEV, generator=torch.Generator(DEV).manual_seed(43),
+                    dtype=torch.bfloat16).transpose(1, 2)
+    w = (1 + 0.02 * torch.randn(D, generator=torch.Generator().manual_seed(44))).to(DEV)
+    base = torch.tensor([0, 7, 64, 3, 50, 1, 33, 12], dtype=torch.int32, device=DEV)
+    lens = torch.tensor([S, S, S - 5, S, 1000, S, S, 17], dtype=torch.int32, device=DEV)
+    ids = (base[:, None].long() + torch.arange(S, device=DEV)[None, :])
+    kw = dict(q_weight=w, eps=1e-6, cos=cos, sin=sin, causal=False, return_lse=True, key_lens=lens)
+    o_base, l_base = nq.attention_prefill(q, k, v, pos_base=base, **kw)
+    o_ids, l_ids = nq.attention_prefill(q, k, v, position_ids=ids, **kw)
+    assert torch.isfinite(o_base).all()
+    assert torch.equal(o_base, o_ids) and torch.equal(l_base, l_ids), \
+        f"max |diff| {(o_base.float() - o_ids.float()).abs().max().item():.3e}"
+    kw["key_lens"] = None
+    kw["causal"] = True
+    o_off, _ = nq.attention_prefill(q, k, v, pos_offset=5, **kw)
+    o_ids5, _ = nq.attention_prefill(q, k, v, position_ids=torch.arange(S, device=DEV)[None, :].expand(B, S) + 5,
+                                     **kw)
+    assert torch.equal(o_off, o_ids5), f"max |diff| {(o_off.float() - o_ids5.float()).abs().max().item():.3e}"
