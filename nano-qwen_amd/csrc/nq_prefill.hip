@@ -239,11 +239,20 @@ prefill_kernel(PrefillParams p) {
   load_k(0, 0);
   load_v(0, 0);
   if (ntiles > 1) load_k(1, 1);
+  // A wave reads the table rows of its own 32 / G positions.  When those fill
+  // whole DMA instructions the wave stages exactly them and then waits for its
+  // own loads only; otherwise the instructions are spread over the waves and a
+  // barrier follows (8B-like shape: that barrier waited ~1.7 us for the
+  // slowest wave).
+  constexpr int TROW = D * 2;  // bytes per table row
+  const int tab_rpw = 32 / p.G;
+  const bool tab_own = stage_tab && tab_rpw > 0 && tab_rpw % (1024 / TROW) == 0;  // G = 64: 0 rows
   if (stage_tab) {
     const int pos0 = (p.q_pos_base ? ld_uniform(p.q_pos_base, b) : p.q_pos0) + q0;
-    constexpr int TROW = D * 2;  // bytes per table row
     const int ninst = (p.BM * TROW + 1023) / 1024;
-    for (int m = wave; m < ninst; m += NW) {
+    const int m0 = tab_own ? wave * tab_rpw * TROW / 1024 : wave;
+    const int m1 = tab_own ? (wave + 1) * tab_rpw * TROW / 1024 : ninst;
+    for (int m = m0; m < m1; m += tab_own ? 1 : NW) {
       const int pb = m * 1024 + lane * 16;
       const int row = pb / TROW;
       const int c = Tl::k_chunk(row, (pb % TROW) / 16);  // logical 16-byte chunk (4 values)
@@ -261,7 +270,7 @@ prefill_kernel(PrefillParams p) {
     if (do_rope) {
       if (stage_tab) {
         wait_vmcnt0();
-        __syncthreads();
+        if (!tab_own) __syncthreads();
         // row pr of the stage; a position outside the tables gives NaN, as the
         // per-lane loads do
         const float bad = tab_row < 0 ? __builtin_nanf("") : 0.f;
