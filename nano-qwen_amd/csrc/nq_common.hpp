@@ -316,15 +316,16 @@ __device__ __forceinline__ void norm_rope_row(floatx8& x1, floatx8& x2, const fl
   }
 }
 
-// Position of (b, s): explicit positions win, else base[b] + s, else pos0 + s.
-// A wave-uniform element of a read-only input, read through the scalar path
-// (s_load; the address space says the kernel never writes it).  As a vector
-// load, a conditional one like pos_base[b] left an s_waitcnt vmcnt(0) where
-// its paths merged, which drained every tile load issued before it.
+// An element of a read-only input (the address space says the kernel never
+// writes it): a wave-uniform index reads through the scalar path (s_load), a
+// per-lane one still becomes a vector load.  As a vector load, a conditional
+// wave-uniform read like pos_base[b] left an s_waitcnt vmcnt(0) where its
+// paths merged, which drained every tile load issued before it.
 __device__ __forceinline__ int32_t ld_uniform(const int32_t* base, int64_t i) {
   return ((const __attribute__((address_space(4))) int32_t*)base)[i];
 }
 
+// Position of (b, s): explicit positions win, else base[b] + s, else pos0 + s.
 __device__ __forceinline__ int row_position(const int32_t* pos, const int32_t* pos_base, int pos0,
                                             int b, int s, int S) {
   if (pos) return pos[(int64_t)b * S + s];
