@@ -10,7 +10,8 @@
  *   - A "row" is head_dim contiguous elements.  4-D tensors are described by
  *     their base pointer plus three element strides for the (batch, head,
  *     sequence) axes; the head_dim axis must be contiguous.  Base pointers must
- *     be 16-byte aligned and strides multiples of 16 bytes.
+ *     be 16-byte aligned and strides multiples of 16 bytes.  So must the fp32
+ *     cos/sin tables given to nq_attn_prefill_fwd (rows go to LDS by DMA).
  *   - dtype codes: NQ_DTYPE_BF16 (bfloat16 stored as 16-bit words) or
  *     NQ_DTYPE_F32.  bf16 data: matrix products on bf16 MFMA with fp32
  *     accumulation.  fp32 data in nq_attn_prefill_fwd: products on fp32 MFMA

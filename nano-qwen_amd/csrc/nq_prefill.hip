@@ -711,6 +711,8 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
       return nq_fail(NQ_ERR_UNSUPPORTED, "k/v sequence stride %lld too large", (long long)s[2]);
   if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
+  if (!nq_aligned16(cos_tab) || !nq_aligned16(sin_tab))  // their rows are DMA'd to LDS in 16-byte pieces
+    return nq_fail(NQ_ERR_INVALID, "cos/sin tables must be 16-byte aligned");
   PrefillParams p{};
   p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse;
   p.qsb = q_strides[0]; p.qsh = q_strides[1]; p.qss = q_strides[2];

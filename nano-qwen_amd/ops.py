@@ -84,8 +84,11 @@ def _rows_out(t: torch.Tensor, name: str) -> torch.Tensor:
 def _f32(t: Optional[torch.Tensor], device) -> Optional[torch.Tensor]:
     if t is None:
         return None
-    if t.dtype != torch.float32 or t.device != device or not t.is_contiguous():
+    if (t.dtype != torch.float32 or t.device != device or not t.is_contiguous()
+            or t.data_ptr() % 16):  # the kernels DMA weights and table rows in 16-byte pieces
         t = t.to(device=device, dtype=torch.float32).contiguous()
+        if t.data_ptr() % 16:
+            t = t.clone()
     return t
 
 

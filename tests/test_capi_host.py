@@ -55,6 +55,13 @@ def test_argument_errors_need_no_gpu():
                                  1, 8, 2, 8, 4, 128, 0, None, 1e-6, None, None, 0,
                                  None, None, 0, 1, 0.0, None)
     assert rc == _lib.NQ_ERR_INVALID and b"S <= T" in lib.nq_last_error()
+    # table rows are DMA'd to LDS in 16-byte pieces: a misaligned table is refused
+    # (never dereferenced: the check precedes every launch)
+    a, odd = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 4)
+    rc = lib.nq_attn_prefill_fwd(a, st, a, st, a, st, a, st, None, None,
+                                 1, 8, 2, 8, 8, 128, 0, None, 1e-6, odd, a, 16,
+                                 None, None, 0, 1, 0.0, None)
+    assert rc == _lib.NQ_ERR_INVALID and b"aligned" in lib.nq_last_error()
     # slots = waves + rows; a slot holds 16 heads x (D outputs + max + sum) in
     # fp32, and each row records its first and last covering wave (2 x int32)
     slot = 16 * 130 * 4
@@ -70,6 +77,19 @@ def test_argument_errors_need_no_gpu():
                                 2, 8, 2, 128, 5000, 1024, 0, None, 1e-6, None, None, 0,
                                 None, -1, 0.0, None)
     assert rc == _lib.NQ_ERR_INVALID
+
+
+def test_fp32_side_inputs_are_realigned():
+    """Norm weights and tables handed to the kernels start on 16-byte boundaries:
+    a contiguous fp32 view at an odd offset is copied, an aligned one passed as is."""
+    from nano_qwen_amd.ops import _f32
+    base = torch.arange(40, dtype=torch.float32)
+    view = base[1:33]
+    assert view.is_contiguous() and view.data_ptr() % 16
+    out = _f32(view, base.device)
+    assert out.data_ptr() % 16 == 0 and torch.equal(out, view)
+    aligned = base[4:36]
+    assert _f32(aligned, base.device).data_ptr() == aligned.data_ptr()
 
 
 def test_cpu_tensors_are_refused():
