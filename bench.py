@@ -227,9 +227,11 @@ class Backward:
     def __init__(self, nq, name, B, S, Hq, Hkv, D, seed, device="cuda"):
         self.nq, self.name = nq, name
         self.B, self.S, self.Hq, self.Hkv, self.D = B, S, Hq, Hkv, D
-        # the attention's operands after QK-Norm + RoPE, in the projections' layout
-        self.q = _randn((B, S, Hq, D), seed, device).transpose(1, 2)
-        self.k = _randn((B, S, Hkv, D), seed + 100, device).transpose(1, 2)
+        # the attention's operands after QK-Norm + RoPE as the training path holds them:
+        # Q-hat and K-hat head-major (the row kernel's outputs), V and dO in the
+        # projections' (B, S, H, D) storage
+        self.q = _randn((B, S, Hq, D), seed, device).transpose(1, 2).contiguous()
+        self.k = _randn((B, S, Hkv, D), seed + 100, device).transpose(1, 2).contiguous()
         self.v = _randn((B, S, Hkv, D), seed + 200, device).transpose(1, 2)
         self.do = _randn((B, S, Hq, D), seed + 400, device).transpose(1, 2)
         self.o, self.lse = nq.attention_prefill(self.q, self.k, self.v, causal=True, return_lse=True)
