@@ -82,7 +82,7 @@ class Prefill:
         self.kw = (1 + wscale * torch.randn(D, generator=g)).to(device)
         cos, sin = nq.build_tables(D, S, 1e6, rope_scaling)
         self.cos, self.sin = cos.to(device), sin.to(device)
-        self.khat = torch.empty(B, Hkv, S, D, dtype=torch.bfloat16, device=device)  # as the module allocates it
+        self.khat = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
         self.out = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
         self.work = 4.0 * D * B * Hq * S * (S + 1) / 2
         self.rope_scaling = rope_scaling
