@@ -563,6 +563,9 @@ __global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p
   const int kvh = j / p.NG, hg = j % p.NG;
   const int hq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * DPT;
   const int gh = hg * 16 + hq;
+  // the row's first and last covering wave, read through the scalar path
+  // alongside lens[b] (a row without keys never uses them)
+  const int64_t wf = ld_uniform(p.ws_rw, r * 2), wl = ld_uniform(p.ws_rw, r * 2 + 1);
   const int len = uniform(batch_len(p, b));
   if (p.lens_out && j == 0 && threadIdx.x == 0) p.lens_out[b] = len < 0 ? p.lens[b] : p.lens[b] + 1;
   T* orow = reinterpret_cast<T*>(p.o) + b * p.osb + (int64_t)(kvh * p.G + (gh < p.G ? gh : 0)) * p.osh + d0;
@@ -575,34 +578,39 @@ __global__ void __launch_bounds__(DC_THREADS) decode_merge_kernel(DecodeParams p
     }
     return;
   }
-  const int64_t wf = uniform(p.ws_rw[r * 2]), wl = uniform(p.ws_rw[r * 2 + 1]);
   if (wf == wl || gh >= p.G) return;  // one wave covered the row and wrote it
   const float* ml = p.ws_ml + ((wf + r) * 16 + hq) * 2;
   const float* po = p.ws_o + ((wf + r) * 16 + hq) * D + d0;
   const int ns = (int)(wl - wf + 1);
-  float M = -INFINITY;
-  for (int i = 0; i < ns; ++i) M = fmaxf(M, ml[i * 32]);
-  float wsum = 0.f;
+  // one pass with a running max, so every partial's (m, l) and outputs are
+  // loaded together (every partial holds at least one key: its m is finite)
+  float M = -INFINITY, wsum = 0.f;
   float acc[DPT];
 #pragma unroll
   for (int e = 0; e < DPT; ++e) acc[e] = 0.f;
 #pragma unroll 4
   for (int i = 0; i < ns; ++i) {
     const floatx2 m_l = *reinterpret_cast<const floatx2*>(ml + i * 32);
-    const float sc = fast_exp2(m_l[0] - M);
-    wsum += m_l[1] * sc;
+    float o[DPT];
     if constexpr (DPT == 2) {
       const floatx2 o2 = *reinterpret_cast<const floatx2*>(po + (int64_t)i * 16 * D);
-      acc[0] += o2[0] * sc;
-      acc[1] += o2[1] * sc;
+      o[0] = o2[0];
+      o[1] = o2[1];
     } else {
 #pragma unroll
       for (int e = 0; e < DPT; e += 4) {
         const floatx4 o4 = *reinterpret_cast<const floatx4*>(po + (int64_t)i * 16 * D + e);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[e + k] += o4[k] * sc;
+        for (int k = 0; k < 4; ++k) o[e + k] = o4[k];
       }
     }
+    const float Mn = fmaxf(M, m_l[0]);
+    const float a = fast_exp2(M - Mn);  // 0 for the first partial
+    const float sc = fast_exp2(m_l[0] - Mn);
+    wsum = wsum * a + m_l[1] * sc;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[e] = acc[e] * a + o[e] * sc;
+    M = Mn;
   }
   const float inv = 1.0f / wsum;
   if constexpr (DPT == 8) {
