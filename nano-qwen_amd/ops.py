@@ -684,15 +684,19 @@ def qk_norm_rope_backward(x: torch.Tensor, dy: torch.Tensor, *, weight: Optional
 # ---------------------------------------------------------------------------
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
-                    sm_scale: Optional[float] = None) -> torch.Tensor:
+                    sm_scale: Optional[float] = None, use_triton: bool = True) -> torch.Tensor:
     """kernels/flash_attn.py:130-143 on the gfx950 prefill kernel.
 
     q: (B, H, N, D), k/v: (B, Hkv, N, D) with H % Hkv == 0 (the reference
     requires Hkv == H; GQA is accepted here).  Where the reference hands inputs
     that require grad to torch's SDPA (flash_attn.py:139), this runs them
     through the kernels' autograd Function (FlashAttention-2 backward).
+    ``use_triton`` is accepted for signature compatibility (flash_attn.py:136)
+    and selects nothing: the HIP kernels are the only backend, so True and
+    False give the same bits.
     Returns a contiguous (B, H, N, D) tensor.
     """
+    del use_triton
     _require_device(q, k, v)
     if q.numel() == 0:
         # no query rows: an empty output, as the reference's grid of zero blocks gives
@@ -705,12 +709,15 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
 
 
 def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
-               sin: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+               sin: torch.Tensor, use_triton: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
     """kernels/rope.py:99-108: rotate-half RoPE of q and k, in place.
 
     q: (B, Hq, S, D), k: (B, Hk, S, D); cos/sin: (S, D/2) rows for positions
     0..S-1, or (B, S, D/2) per-batch rows.  Arithmetic is fp32.
+    ``use_triton`` is accepted for signature compatibility (rope.py:104) and
+    selects nothing: the row kernel is the only backend.
     """
+    del use_triton
     _require_device(q, k)
     B, _, S, D = q.shape
     if cos.dim() == 3:

@@ -466,3 +466,32 @@ def test_plain_cache_step_is_one_fused_call_and_bit_equal():
     assert torch.equal(kc[:, :, :51], kc0[:, :, :51]) and torch.equal(vc[:, :, :51], vc0[:, :, :51])
     assert torch.equal(out, attn.o_proj(o.reshape(B, 1, H * D)))
     assert cache.seq_len == 51
+
+
+# ------------------------------------------------------------------ use_triton keyword
+
+@torch.no_grad()
+def test_use_triton_keyword_selects_nothing():
+    """kernels/flash_attn.py:136 and kernels/rope.py:104 take use_triton; the
+    mirrors accept it and give the same bits for True and False."""
+    say("use_triton keyword: flash_attention / apply_rope")
+    B, S, H, D = 2, 200, 4, 128
+    q = randn(B, H, S, D, seed=4101, dtype=torch.bfloat16).to(DEV)
+    k = randn(B, H, S, D, seed=4102, dtype=torch.bfloat16).to(DEV)
+    v = randn(B, H, S, D, seed=4103, dtype=torch.bfloat16).to(DEV)
+    outs = [nq.flash_attention(q, k, v, causal=True, use_triton=ut) for ut in (True, False)]
+    outs.append(nq.flash_attention(q, k, v, True, None, False))  # positional, as the reference allows
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ref = attention(q.float().cpu(), k.float().cpu(), v.float().cpu(), causal=True)
+    assert_bf16_close(outs[0], ref, "flash_attention")
+    cos, sin = rope_tables(D, S, 1e6)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    rot = []
+    for ut in (True, False):
+        qq, kk = q.clone(), k.clone()
+        r = nq.apply_rope(qq, kk, cos, sin, use_triton=ut)
+        assert r[0] is qq and r[1] is kk  # in place, as kernels/rope.py does
+        rot.append((qq, kk))
+    assert torch.equal(rot[0][0], rot[1][0]) and torch.equal(rot[0][1], rot[1][1])
+    c, s = cos.cpu()[None, None], sin.cpu()[None, None]
+    assert_bf16_close(rot[0][0], rotate_half(q.float().cpu(), c, s), "apply_rope q")
