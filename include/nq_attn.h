@@ -162,7 +162,8 @@ int64_t nq_attn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int max_le
  *   every row, or lens[b] - 1 when q_pos0 < 0.
  * o: output (B, Hq, D) with strides {batch, head}.
  * workspace: device buffer of at least
- *   nq_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk) bytes.
+ *   nq_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk) bytes for
+ *   bf16 caches; fp32 caches keep no partials and ignore it (NULL allowed).
  * Requires Hq / Hkv <= 16 or a multiple of 16.
  */
 int nq_attn_decode_fwd(const void* q, const int64_t* q_strides, const void* k_cache,
@@ -225,7 +226,8 @@ int nq_attn_decode_paged_fwd(const void* q, const int64_t* q_strides, const void
  * of NQ_DECODE_SCRATCH_BYTES that each GPU the library runs on holds until
  * the process ends; sizes whose workspace
  * (nq_attn_decode_workspace_bytes) exceeds it are refused with
- * NQ_ERR_WORKSPACE.  The caller still passes every input and output.  All
+ * NQ_ERR_WORKSPACE (fp32 caches use no workspace and are never refused for
+ * it).  The caller still passes every input and output.  All
  * calls on one GPU share that GPU's array: calls that overlap on one GPU (on
  * different streams, or from different threads) race.  Results are those of
  * nq_attn_decode_paged_fwd with the same arguments.

@@ -751,6 +751,11 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   for (const int64_t rs : {q_strides[2], do_strides[2]})
     if (rs < 0 || rs * esz * 32 >= (int64_t(1) << 31))
       return nq_fail(NQ_ERR_UNSUPPORTED, "q and dout position strides must lie in [0, 2^26 / element size)");
+  // the dQ kernel stages 64-key K/V tiles through a buffer descriptor whose
+  // range and lane offsets are 32-bit (as the prefill's tiles)
+  for (const int64_t rs : {k_strides[2], v_strides[2]})
+    if (rs < 0 || rs * esz * BW_BN >= (int64_t(1) << 31))
+      return nq_fail(NQ_ERR_UNSUPPORTED, "k/v sequence stride %lld too large", (long long)rs);
   if (!lse) return nq_fail(NQ_ERR_INVALID, "the forward's LSE is required");
   const int64_t need = nq_attn_bwd_workspace_bytes(B, Hq, S);
   if (!workspace || workspace_bytes < need)

@@ -699,8 +699,11 @@ static int decode_setup(DecodeParams& p, const void* q, const int64_t* q_strides
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
   if (k_strides[2] < D || v_strides[2] < D)
     return nq_fail(NQ_ERR_INVALID, "cache rows must not overlap (seq stride >= head_dim)");
+  // fp32 caches run the fp32 prefill kernel at S = 1, which keeps no partials:
+  // the workspace is neither required nor read there
+  const bool f32 = dtype == NQ_DTYPE_F32;
   const int64_t need = dc_workspace(B, Hq, Hkv, D, max_len, chunk);
-  if (workspace == nullptr || workspace_bytes < need)
+  if (!f32 && (workspace == nullptr || workspace_bytes < need))
     return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
                    (long long)workspace_bytes);
   p.q = q; p.qsb = q_strides[0]; p.qsh = q_strides[1];
@@ -716,9 +719,11 @@ static int decode_setup(DecodeParams& p, const void* q, const int64_t* q_strides
   const int64_t nw = dc_waves(B, Hkv, p.NG, max_len, chunk);
   if (nw / DC_WAVES > 0x7fffffff) return nq_fail(NQ_ERR_INVALID, "chunk %d too small for these sizes", chunk);
   p.nwaves = (int)nw;
-  p.ws_o = reinterpret_cast<float*>(workspace);
-  p.ws_ml = p.ws_o + (nw + (int64_t)B * p.rows_per_batch) * 16 * D;
-  p.ws_rw = reinterpret_cast<int32_t*>(p.ws_ml + (nw + (int64_t)B * p.rows_per_batch) * 16 * 2);
+  if (!f32) {
+    p.ws_o = reinterpret_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (nw + (int64_t)B * p.rows_per_batch) * 16 * D;
+    p.ws_rw = reinterpret_cast<int32_t*>(p.ws_ml + (nw + (int64_t)B * p.rows_per_batch) * 16 * 2);
+  }
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
   return NQ_OK;
@@ -953,9 +958,11 @@ extern "C" int nq_attn_decode_paged_fwd_noalloc(
     const float* q_weight, float eps, const float* cos_tab, const float* sin_tab, int max_pos,
     const int32_t* q_pos, int q_pos0, float sm_scale, void* stream) {
   nq_clear_error();
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0 || Hq % Hkv || !head_dim_ok(D))
-    return nq_fail(NQ_ERR_INVALID, "invalid sizes (B=%d Hq=%d Hkv=%d D=%d max_len=%d)", B, Hq, Hkv, D, max_len);
-  const int64_t need = dc_workspace(B, Hq, Hkv, D, max_len, chunk);
+  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0 || Hq % Hkv)
+    return nq_fail(NQ_ERR_INVALID, "invalid sizes (B=%d Hq=%d Hkv=%d max_len=%d)", B, Hq, Hkv, max_len);
+  // fp32 caches keep no partials (the workspace is unused), so any size is served
+  const int64_t need = dtype == NQ_DTYPE_F32 ? 0 : dc_workspace(B, Hq, Hkv, D, max_len, chunk);
   if (need > NQ_DECODE_SCRATCH_BYTES)
     return nq_fail(NQ_ERR_WORKSPACE,
                    "these sizes need %lld bytes of workspace, more than the %lld of the static scratch; "

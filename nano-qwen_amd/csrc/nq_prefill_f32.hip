@@ -65,7 +65,10 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
   const int q0 = qblk * p.BM;
   // keys of this sequence (-1: a length out of range, no keys and NaN rows)
   const int T = pf_keys(p, b);
-  const int coff = T - p.S;
+  // the causal frontier is bottom-right against the launch's T (query i keeps
+  // keys j <= i + p.T - p.S); key_lens only shortens the key range, as in the
+  // bf16 kernel and the backward
+  const int coff = p.T - p.S;
   const int kv_end = max(0, CAUSAL ? min(T, q0 + p.BM + coff) : T);
   const int ntiles = (kv_end + PF32_BN - 1) / PF32_BN;
 

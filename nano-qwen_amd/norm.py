@@ -5,7 +5,10 @@ fp32.  The module's own ``forward`` runs ``nq_rmsnorm``: rows of any width (a
 multiple of 8), the reference's cast order (the normalised value is cast back
 to ``x.dtype`` before the weight multiply) and its dtype promotion (a bf16
 input with an fp32 weight gives fp32, as ``output.type_as(x) * weight`` does).
-Under autograd the backward is ``nq_qk_norm_rope_bwd`` (widths 32, 64, 128).
+Under autograd dx comes from ``nq_qk_norm_rope_bwd`` at widths 32, 64 and 128
+(QK-Norm's head dims) and from a torch composition of the same formula at other
+widths (the model's hidden-size norms); the weight gradient is reduced from the
+incoming gradient in fp32, as the reference's autograd does.
 """
 
 from __future__ import annotations
@@ -44,12 +47,26 @@ class _RMSNormFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy):
+        # y = n.to(x.dtype) * w with n = x * rsqrt(mean(x^2) + eps) in fp32
+        # (model/norm.py:17-22).  dw = sum over rows of dy * n.to(x.dtype), in
+        # fp32 from dy as it arrives; dx = r * (g - n * mean(g * n)) with g the
+        # gradient of the cast value, (dy * w) in x's dtype.
         x, weight = ctx.saved_tensors
         W = x.shape[-1]
-        x4 = x.reshape(1, 1, -1, W)
-        dy4 = dy.to(x.dtype).reshape(1, 1, -1, W)
-        dx, dw = ops.qk_norm_rope_backward(x4, dy4, weight=weight, eps=ctx.eps)
-        return dx.reshape(x.shape), dw.to(weight.dtype), None
+        ones = torch.ones(W, dtype=torch.float32, device=x.device)
+        ncast = rms_norm(x, ones, ctx.eps)  # n.to(x.dtype), held in fp32 exactly
+        dw = (dy.float() * ncast).reshape(-1, W).sum(0).to(weight.dtype)
+        if W in (32, 64, 128):
+            x4 = x.reshape(1, 1, -1, W)
+            dy4 = dy.to(x.dtype).reshape(1, 1, -1, W)
+            dx, _ = ops.qk_norm_rope_backward(x4, dy4, weight=weight, eps=ctx.eps)
+            return dx.reshape(x.shape), dw, None
+        xf = x.float()
+        r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + ctx.eps)
+        n = xf * r
+        g = (dy * weight).to(x.dtype).float()
+        dx = r * (g - n * (g * n).mean(-1, keepdim=True))
+        return dx.to(x.dtype), dw, None
 
 
 class RMSNorm(nn.Module):
@@ -60,7 +77,5 @@ class RMSNorm(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
-            if x.shape[-1] not in (32, 64, 128):
-                raise NotImplementedError("RMSNorm's backward kernel covers widths 32, 64 and 128")
             return _RMSNormFn.apply(x, self.weight, self.eps)
         return rms_norm(x, self.weight, self.eps)

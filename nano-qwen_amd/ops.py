@@ -381,7 +381,8 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     if out is None:
         out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
     dev = q.device
-    need = decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk)
+    # fp32 caches keep no partials: the library neither needs nor reads a workspace
+    need = 0 if q.dtype == torch.float32 else decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
@@ -539,7 +540,8 @@ def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
             raise ValueError("lens_out must not alias lens")
     if out is None:
         out = torch.empty(B, Hq, D, dtype=q.dtype, device=dev)
-    need = decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk)
+    # fp32 caches keep no partials: the library neither needs nor reads a workspace
+    need = 0 if q.dtype == torch.float32 else decode_workspace_bytes(B, Hq, Hkv, D, max_len, chunk)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()

@@ -77,6 +77,12 @@ def test_argument_errors_need_no_gpu():
                                 2, 8, 2, 128, 5000, 1024, 0, None, 1e-6, None, None, 0,
                                 None, -1, 0.0, None)
     assert rc == _lib.NQ_ERR_INVALID
+    # the no-allocation decode reports an unsupported head_dim as the others do
+    z = _lib.strides3((0, 0, 0))
+    rc = lib.nq_attn_decode_paged_fwd_noalloc(
+        None, z, None, None, None, None, None, None, z, None, z, None, 1, 32, None, None, None, z,
+        2, 8, 2, 96, 64, 0, _lib.NQ_DTYPE_BF16, None, 1e-6, None, None, 0, None, -1, 0.0, None)
+    assert rc == _lib.NQ_ERR_UNSUPPORTED and b"head_dim" in lib.nq_last_error()
 
 
 def test_fp32_side_inputs_are_realigned():

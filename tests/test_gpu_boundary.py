@@ -331,6 +331,35 @@ def test_rmsnorm_mirror_promotion_and_widths(width, xdt, wdt):
     torch.testing.assert_close(y.float().cpu(), ref.float(), rtol=tol, atol=tol)
 
 
+@pytest.mark.parametrize("width", [64, 256, 2048])
+@pytest.mark.parametrize("xdt,wdt", [(torch.bfloat16, torch.float32), (torch.float32, torch.float32)])
+def test_rmsnorm_mirror_autograd_any_width(width, xdt, wdt):
+    """RMSNorm under autograd at QK-Norm widths and hidden-size widths: the
+    gradients of the reference's composition (norm.py:17-22, autograd on the
+    CPU with the same casts), dw reduced from the fp32 incoming gradient."""
+    say(f"RMSNorm autograd width={width} x={xdt} w={wdt}")
+    x = randn(4, 7, width, seed=3331, dtype=xdt)
+    w0 = 1 + 0.1 * randn(width, seed=3332)
+    dy = randn(4, 7, width, seed=3333)
+    norm = nq.RMSNorm(width, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(w0)
+    norm = norm.to(DEV, wdt)
+    xd = x.to(DEV).requires_grad_(True)
+    y = norm(xd)
+    y.backward(dy.to(DEV, y.dtype))
+    xr = x.clone().requires_grad_(True)
+    wr = w0.to(wdt).clone().requires_grad_(True)
+    yr = rms_norm(xr, wr, 1e-6)
+    yr.backward(dy.to(yr.dtype))
+    assert y.dtype == yr.dtype
+    tol = 1e-5 if xdt == torch.float32 else 2e-2
+    torch.testing.assert_close(y.detach().float().cpu(), yr.detach().float(), rtol=tol, atol=tol)
+    torch.testing.assert_close(xd.grad.float().cpu(), xr.grad.float(), rtol=tol, atol=tol)
+    sc = float(wr.grad.abs().max())
+    torch.testing.assert_close(norm.weight.grad.float().cpu(), wr.grad.float(), rtol=0, atol=1e-4 * sc)
+
+
 # ------------------------------------------------------------------ decode positions, overflow
 
 def test_decode_position_ids_broadcast():

@@ -92,6 +92,43 @@ def test_backward_key_lens(dtype, D):
         assert not dk[b, :, L:].float().abs().any() and not dv[b, :, L:].float().abs().any()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("T", [130, 161])
+def test_causal_with_key_lens_forward_and_backward(dtype, D, T):
+    """Causal attention with per-sequence key counts: the frontier is
+    bottom-right against the launch's T (query i keeps keys j <= i + T - S) and
+    key_lens only shortens the key range, in the fp32 and bf16 kernels alike,
+    forward and backward.  Rows before a short sequence's first key are the
+    case an offset taken from key_lens instead of T would turn into NaN."""
+    say(f"causal + key_lens {dtype} D={D} T={T}")
+    B, Hq, Hkv, S = 3, 8, 2, 130
+    lens = torch.tensor([T, 3, 90], dtype=torch.int32)
+    q = randn(B, Hq, S, D, seed=741, dtype=dtype)
+    k = _poison(randn(B, Hkv, T, D, seed=742, dtype=dtype), lens)
+    v = _poison(randn(B, Hkv, T, D, seed=743, dtype=dtype), lens)
+    do = randn(B, Hq, S, D, seed=744, dtype=dtype)
+    kl = lens.to(DEV)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, key_lens=kl, return_lse=True)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(lse).all()
+    ref = attention(q.float(), k.float().nan_to_num(), v.float().nan_to_num(), causal=True,
+                    causal_offset=T - S, key_lens=lens)
+    assert_close_for(dtype, o, ref, "causal + key_lens forward")
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=True,
+                                        key_lens=kl)
+    qd, kd, vd = (t.double().nan_to_num().requires_grad_(True) for t in (q, k, v))
+    attention(qd, kd, vd, causal=True, causal_offset=T - S, key_lens=lens,
+              compute_dtype=torch.float64).backward(do.double())
+    mx_tol, mean_tol = (1e-5, 1e-6) if dtype == torch.float32 else (2e-2, 2e-3)
+    for got, want, name in ((dq, qd.grad, "dq"), (dk, kd.grad, "dk"), (dv, vd.grad, "dv")):
+        got = got.double().cpu()
+        assert torch.isfinite(got).all(), name
+        sc = float(want.abs().max())
+        d = (got - want).abs()
+        assert float(d.max()) <= mx_tol * sc and float(d.mean()) <= mean_tol * sc, \
+            f"{name}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {sc:.3e})"
+
+
 def _module(dtype, seed=731):
     cfg = nq.AttentionConfig(hidden_size=256, num_attention_heads=8, num_key_value_heads=2, head_dim=64,
                              max_position_embeddings=512)
