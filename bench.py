@@ -8,7 +8,10 @@ seeded inputs already resident in HBM:
            (Q-Norm + RoPE on load, causal GQA FlashAttention forward);
   decode   append of the new token's K-hat/V into the cache, then the decode
            kernel (a persistent grid streaming the ragged cache) and its merge;
-           the paged form fuses the append into the decode launch.
+           the paged form fuses the append into the decode launch;
+  chunk    a prompt continuation into a paged cache: the chunk's K-hat/V
+           appended into its pages, then the paged prefill kernel over all
+           keys so far through the block table (no dense copy).
 The headline ``value`` is prefill TFLOP/s on the Qwen3-1.7B-like layer
 (B8 S2048 Hq16 Hkv8 D128 causal bf16); FLOPs are the algorithmic
 4*D*B*Hq*S(S+1)/2 (QK^T + PV over causal pairs).  ``roofline`` divides the
@@ -17,7 +20,8 @@ back on its launch stream between two HIP events, after the K timed steps
 (``ms_per_step``, with nothing between the launches).  ``secondary`` holds
 the other workloads, each with its roofline (decode bytes
 sum_b 2*Hkv*T_b*D*2 + 2*B*Hq*D*2; backward FLOPs 2.5x the forward's, the five
-matrix products of FlashAttention-2).
+matrix products of FlashAttention-2; chunk FLOPs 4*D*B*Hq*(C*p0 + C(C+1)/2)
+for C queries after p0 cached keys).
 Before its W warmup and K timed steps, each workload runs its own step
 untimed for ``--settle-s`` seconds (default 0.2): the GPU raises its clock over
 the first ~40 ms of sustained load (the 1.7B-like step goes from ~0.20 to
@@ -218,6 +222,66 @@ class PagedDecode(Decode):
         d = super().describe()
         d["cache"] = f"paged, {self.page}-row pages in a seeded random order, append fused"
         return d
+
+
+class PagedChunk:
+    """One chunk of a chunked prefill into a paged cache: the last 2048 tokens of 8192-token
+    sequences whose first 6144 keys already sit in 64-row pages dealt in a seeded random
+    order.  A step appends the chunk's K-hat (norm and rotation fused) and V into its pages,
+    then the chunk's queries attend all keys through the block table (causal, true
+    positions)."""
+    kind = "prefill"
+
+    def __init__(self, nq, name, B, T, C, Hq, Hkv, D, seed, page=64, device="cuda"):
+        self.nq, self.name, self.page = nq, name, page
+        self.B, self.T, self.C, self.Hq, self.Hkv, self.D = B, T, C, Hq, Hkv, D
+        self.p0 = T - C
+        self.q = _randn((B, C, Hq, D), seed, device).transpose(1, 2)
+        self.k = _randn((B, C, Hkv, D), seed + 100, device).transpose(1, 2)
+        self.v = _randn((B, C, Hkv, D), seed + 200, device).transpose(1, 2)
+        g = torch.Generator().manual_seed(seed + 300)
+        self.qw = (1 + 0.02 * torch.randn(D, generator=g)).to(device)
+        self.kw = (1 + 0.02 * torch.randn(D, generator=g)).to(device)
+        cos, sin = nq.build_tables(D, T, 1e6)
+        self.cos, self.sin = cos.to(device), sin.to(device)
+        npp = T // page
+        self.bt = torch.randperm(B * npp, generator=g).view(B, npp).to(torch.int32).to(device)
+        # the cached rows: unit-rms keys (as K-hat is) and N(0,1) values
+        gd = torch.Generator(device=device).manual_seed(seed + 400)
+        kp = torch.randn(B * npp, Hkv, page, D, generator=gd, device=device)
+        self.kp = (kp * torch.rsqrt(kp.pow(2).mean(-1, keepdim=True))).to(torch.bfloat16)
+        self.vp = torch.randn(B * npp, Hkv, page, D, generator=gd, device=device, dtype=torch.bfloat16)
+        self.out = torch.empty(B, C, Hq, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
+        self.work = 4.0 * D * B * Hq * (C * self.p0 + C * (C + 1) / 2)
+        self.a_call = nq.kv_append_paged(self.k, self.v, self.kp, self.vp, self.bt, k_weight=self.kw,
+                                         eps=1e-6, cos=self.cos, sin=self.sin, row_offset=self.p0,
+                                         pos_offset=self.p0, plan=True)
+        self.p_call = nq.attention_prefill_paged(self.q, self.kp, self.vp, self.bt, T=T, q_weight=self.qw,
+                                                 eps=1e-6, cos=self.cos, sin=self.sin, causal=True,
+                                                 pos_offset=self.p0, out=self.out, plan=True)
+
+    def step(self):
+        self.a_call.launch()
+        self.p_call.launch()
+
+    def timed_launch(self):
+        """The paged prefill (the append rewrites the same rows every step)."""
+        self.p_call.launch()
+
+    def describe(self):
+        return {"workload": self.name, "batch": self.B, "seq_len": self.T, "chunk": self.C,
+                "cached_keys": self.p0, "num_heads": self.Hq, "num_kv_heads": self.Hkv,
+                "head_dim": self.D, "causal": True, "rope": "theta 1e6",
+                "cache": f"paged, {self.page}-row pages in a seeded random order"}
+
+    def roofline(self, kernel_ms, traffic=None):
+        ach = self.work / (kernel_ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "kernel": "prefill_kernel (paged)", "kernel_ms": round(kernel_ms, 5)}
+
+    def throughput(self, step_ms):
+        return self.work / (step_ms * 1e-3) / 1e12, "TFLOP/s"
 
 
 class Backward:
@@ -458,7 +522,38 @@ def cpu_backward(w, rows=None):
     return out
 
 
+def cpu_chunk(w):
+    """The reference's composition of a prompt continuation (norm + RoPE of the chunk,
+    KVCache concatenation after the cached rows, repeat_interleave, SDPA with the
+    bottom-right causal mask) in fp32 on the host cores, over the workload's own
+    inputs and cached rows (gathered from the pages), one batch row at a time."""
+    from oracle import reference_chunk_sdpa
+    B, P, p0 = w.B, w.page, w.p0
+    cos, sin, qw, kw = _cpu(w.cos), _cpu(w.sin), _cpu(w.qw), _cpu(w.kw)
+    pages = w.bt[:, :p0 // P].long()
+
+    def cached(pool, b):
+        return _cpu(pool[pages[b]].permute(1, 0, 2, 3).reshape(1, w.Hkv, p0, w.D))
+
+    dt, passes = 0.0, 0
+    while passes == 0 or dt < CPU_MIN_S:
+        for b in range(B):
+            kc, vc = cached(w.kp, b), cached(w.vp, b)
+            q, k, v = _cpu(w.q[b:b + 1]), _cpu(w.k[b:b + 1]), _cpu(w.v[b:b + 1])
+            t0 = time.perf_counter()
+            reference_chunk_sdpa(q, k, v, kc, vc, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin)
+            dt += time.perf_counter() - t0
+            del kc, vc
+        passes += 1
+    return {"value": round(w.work * passes / dt / 1e12, 4), "unit": "TFLOP/s", **_host(), "kind": "port",
+            "seconds": round(dt, 3), "passes": passes,
+            "sample": f"the full chunk ({B} batch rows, one at a time) x{passes} passes, {dt:.1f} s, fp32; "
+                      "QK-Norm + RoPE of the chunk + cache concatenation + repeat_interleave + SDPA"}
+
+
 def cpu_baseline(name, w):
+    if name == "c3_chunk":
+        return cpu_chunk(w)
     if name in ("c2", "c3"):
         return cpu_prefill(w)
     if name == "c5":
@@ -484,8 +579,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--settle-s", type=float, default=0.2,
                     help="untimed steps for this long before each workload's warmup (GPU clock ramp)")
-    ap.add_argument("--workloads", default="c2,c3,c4,c4_paged,c5,c2_bwd,c3_bwd",
-                    help="comma list of c2 (headline), c3, c4, c4_paged, c5, c2_bwd, c3_bwd")
+    ap.add_argument("--workloads", default="c2,c3,c4,c4_paged,c5,c3_chunk,c2_bwd,c3_bwd",
+                    help="comma list of c2 (headline), c3, c4, c4_paged, c5, c3_chunk, c2_bwd, c3_bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 times), for scaling "
@@ -528,6 +623,10 @@ def main():
         if name == "c5":
             return Prefill(nq, "YaRN long-context prefill B1 S131072 Hq32 Hkv4 D128 causal bf16",
                            1, 131072, 32, 4, 128, seed=1004, rope_scaling=YARN, cpu_gen=False)
+        if name == "c3_chunk":
+            return PagedChunk(nq, "Qwen3-8B-like chunked prefill into a paged cache: the last 2048-token "
+                              "chunk of B4 x 8192, Hq32 Hkv8 D128, causal bf16", 4, 8192, 2048, 32, 8, 128,
+                              seed=1007)
         if name == "c2_bwd":
             return Backward(nq, "Qwen3-1.7B-like attention backward B8 S2048 Hq16 Hkv8 D128 causal bf16",
                             8, 2048, 16, 8, 128, seed=1005)

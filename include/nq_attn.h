@@ -137,6 +137,34 @@ int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                         int causal, float sm_scale, void* stream);
 
 /*
+ * nq_attn_prefill_fwd over K/V held in paged pools: a chunk of S new queries
+ * attends the T keys of its sequence (the T - S already cached plus the S just
+ * appended), read through the block table, so a chunked prefill into a paged
+ * cache never gathers the pages into a dense copy.
+ *
+ * Replaces the concatenation of KVCache.update (model/attention.py:31-38)
+ * followed by SDPA over the whole cache (attention.py:105-115) for a
+ * continuation of the prompt; the reference has no paged cache (the pool
+ * format is the one nq_attn_decode_paged_fwd reads).
+ *
+ * k_pool/v_pool: (num_pages, Hkv, page_size, D) with strides {page, head,
+ *   row}; key t of sequence b is row t % page_size of page
+ *   block_table[b * bt_stride + t / page_size].  page_size % 32 == 0 and
+ *   bt_stride >= ceil(T / page_size).  Every sequence holds T keys.
+ * The other arguments are those of nq_attn_prefill_fwd (no key_lens);
+ * causal keeps key j for query i iff j <= i + T - S.
+ */
+int nq_attn_prefill_paged_fwd(const void* q, const int64_t* q_strides, const void* k_pool,
+                              const int64_t* k_pool_strides, const void* v_pool,
+                              const int64_t* v_pool_strides, const int32_t* block_table,
+                              int64_t bt_stride, int page_size, void* o, const int64_t* o_strides,
+                              float* lse, int B, int Hq, int Hkv, int S, int T, int D, int dtype,
+                              const float* q_weight, float eps, const float* cos_tab,
+                              const float* sin_tab, int max_pos, const int32_t* q_pos,
+                              const int32_t* q_pos_base, int q_pos0, int causal, float sm_scale,
+                              void* stream);
+
+/*
  * Bytes of fp32 workspace nq_attn_decode_fwd needs for these sizes (no
  * counterpart in the reference, whose decode allocates inside torch).
  * max_len bounds every lens[b].  chunk = 0 spreads the cache evenly over a

@@ -28,6 +28,7 @@ token's K/V append fused in) and ``kv_append_paged``.
 
 from .config import AttentionConfig
 from .ops import (apply_rope, attention_decode, attention_decode_paged, attention_prefill,
+                  attention_prefill_paged,
                   decode_workspace_bytes, flash_attention, kv_append_paged, qk_norm_rope)
 from .norm import RMSNorm
 from .rope import RotaryEmbedding, apply_rotary_pos_emb, build_tables
@@ -41,7 +42,7 @@ from .ring import RingAttention, ring_attention_all_ranks, ring_schedule, ring_s
 __all__ = [
     "Attention", "KVCache", "RMSNorm", "RotaryEmbedding", "AttentionConfig",
     "apply_rotary_pos_emb", "build_tables", "flash_attention", "apply_rope",
-    "qk_norm_rope", "attention_prefill", "attention_decode", "decode_workspace_bytes", "stats",
+    "qk_norm_rope", "attention_prefill", "attention_prefill_paged", "attention_decode", "decode_workspace_bytes", "stats",
     "ModelConfig", "Qwen3Model", "TransformerBlock", "TextGenerator", "generate_greedy_batch",
     "PagedKVCache", "attention_decode_paged", "kv_append_paged",
     "attention_merge_", "RingAttention", "ring_step", "ring_schedule", "split_sequence",

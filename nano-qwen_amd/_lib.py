@@ -58,6 +58,17 @@ SIGNATURES = {
         _p, _p, _i32,                                # q_pos, q_pos_base, q_pos0
         _i32, _f32, _p,                              # causal, sm_scale, stream
     ]),
+    "nq_attn_prefill_paged_fwd": (_i32, [
+        _p, _i64p,                                   # q, q_strides
+        _p, _i64p, _p, _i64p,                        # k_pool, v_pool (+ strides)
+        _p, _i64, _i32,                              # block_table, bt_stride, page_size
+        _p, _i64p, _p,                               # o, o_strides, lse
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype
+        _p, _f32,                                    # q_weight, eps
+        _p, _p, _i32,                                # cos, sin, max_pos
+        _p, _p, _i32,                                # q_pos, q_pos_base, q_pos0
+        _i32, _f32, _p,                              # causal, sm_scale, stream
+    ]),
     "nq_attn_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "nq_attn_decode_fwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p,             # q, k_cache, v_cache (+ strides)

@@ -529,20 +529,13 @@ class Attention(nn.Module):
                                       "at the same length")
         p0 = past[0]
         pos = {"position_ids": position_ids} if position_ids is not None else {"pos_offset": p0}
-        if p0 == 0:
-            k_hat = torch.empty(B, S, Hkv, D, dtype=k4.dtype, device=k4.device).transpose(1, 2)
-            ops.qk_norm_rope(k=k4, k_out=k_hat, k_weight=kw, eps=eps, cos=cos, sin=sin, **pos)
-            ops.kv_append_paged(k_hat, v4, cache.k_pool, cache.v_pool, cache.block_table)
-            k_all, v_all = k_hat, v4
-        else:
-            ops.kv_append_paged(k4, v4, cache.k_pool, cache.v_pool, cache.block_table, k_weight=kw,
-                                eps=eps, cos=cos, sin=sin, row_offset=p0, **pos)
-            T, P = p0 + S, cache.page_size
-            pages = cache.block_table[:, :-(-T // P)].long()
-            k_all = cache.k_pool[pages].permute(0, 2, 1, 3, 4).reshape(B, Hkv, -1, D)[:, :, :T]
-            v_all = cache.v_pool[pages].permute(0, 2, 1, 3, 4).reshape(B, Hkv, -1, D)[:, :, :T]
-        o = ops.attention_prefill(q4, k_all, v_all, q_weight=qw, eps=eps, cos=cos, sin=sin,
-                                  causal=True, **pos)
+        # the chunk's K-hat (QK-Norm + RoPE fused) and V rows go into their
+        # pages, then its queries attend all p0 + S keys through the block
+        # table: no dense copy of the cache
+        ops.kv_append_paged(k4, v4, cache.k_pool, cache.v_pool, cache.block_table, k_weight=kw,
+                            eps=eps, cos=cos, sin=sin, row_offset=p0, **pos)
+        o = ops.attention_prefill_paged(q4, cache.k_pool, cache.v_pool, cache.block_table, T=p0 + S,
+                                        q_weight=qw, eps=eps, cos=cos, sin=sin, causal=True, **pos)
         cache.lens.add_(S)
         cache.host_lens = new
         return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))

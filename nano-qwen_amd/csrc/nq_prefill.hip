@@ -113,7 +113,11 @@ struct PfTile {
   __device__ static int v_chunk(int r, int c) { return c ^ (4 * ((r / RPL) & (D / 32 - 1))); }
 };
 
-template <int D, typename T, bool CAUSAL, bool FUSE_Q, int NW>
+// PAGED: K and V rows come from paged pools through the block table (key t of
+// sequence b is row t % page of page bt[b * bts + t / page], pool strides
+// (ksb, ksh, kss) = (page, head, row)); page % 32 == 0, so each 32-row half of
+// a 64-key tile lies in one page.
+template <int D, typename T, bool CAUSAL, bool FUSE_Q, int NW, bool PAGED = false>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW),
                                amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(PrefillParams p) {
@@ -166,12 +170,14 @@ prefill_kernel(PrefillParams p) {
 
   const int kv_end = CAUSAL ? min(Tk, q0 + p.BM + coff) : Tk;
   const int ntiles = (kv_end + PF_BN - 1) / PF_BN;
-  // K/V are bf16 in memory: they go to LDS unconverted
-  const unsigned char* kbase =
-      reinterpret_cast<const unsigned char*>(reinterpret_cast<const bf16*>(p.k) + b * p.ksb + kvh * p.ksh);
-  const unsigned char* vbase =
-      reinterpret_cast<const unsigned char*>(reinterpret_cast<const bf16*>(p.v) + b * p.vsb + kvh * p.vsh);
+  // K/V are bf16 in memory: they go to LDS unconverted.  A paged pool's base
+  // is its kv head's slice of page 0 (pages are added per tile).
+  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(
+      reinterpret_cast<const bf16*>(p.k) + (PAGED ? 0 : b * p.ksb) + kvh * p.ksh);
+  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(
+      reinterpret_cast<const bf16*>(p.v) + (PAGED ? 0 : b * p.vsb) + kvh * p.vsh);
   const int64_t krow_bytes = p.kss * 2, vrow_bytes = p.vss * 2;
+  const int64_t kpage_bytes = p.ksb * 2, vpage_bytes = p.vsb * 2;
 
   // ---- tile loads: load instruction G (0 <= G < NW*LOADS) fills LDS
   // bytes [G*1024, G*1024+1024) of the tile, lane t the 16 bytes at +16*t;
@@ -185,9 +191,43 @@ prefill_kernel(PrefillParams p) {
   const int pc0 = lane % Tl::CPR;
   const uint32_t koff = (uint32_t)(row0 * krow_bytes) + Tl::k_chunk(row0, pc0) * 16;
   const uint32_t voff = (uint32_t)(row0 * vrow_bytes) + Tl::v_chunk(row0, pc0) * 16;
-  auto load_tile = [&](const unsigned char* base, int64_t row_bytes, uint32_t off, int lds_off,
-                       int tile) {
+  auto load_tile = [&](const unsigned char* base, int64_t row_bytes, int64_t page_bytes, uint32_t off,
+                       int lds_off, int tile) {
     const int lds_w = lds_off + wave * 1024;
+    if constexpr (PAGED) {
+      // rows key0 .. key0+31 lie in page pi0 from row r0, rows key0+32 .. +63
+      // in page pi1 from row r1 (page % 32 == 0, key0 % 64 == 0); the block
+      // table is read through the scalar path, only for rows below Tk
+      const int key0 = tile * PF_BN;
+      const int pi0 = key0 / p.page, r0 = key0 - pi0 * p.page;
+      const bool same = r0 + 32 < p.page;
+      const int r1 = same ? r0 + 32 : 0;
+      const int64_t btb = (int64_t)b * p.bts;
+      const int64_t pg0 = ld_uniform(p.bt, btb + pi0);
+      const int64_t pg1 = (same || key0 + 32 >= Tk) ? pg0 : (int64_t)ld_uniform(p.bt, btb + pi0 + 1);
+      if (key0 + PF_BN <= Tk) {
+        // one descriptor per instruction over its RPI rows; the lane's offset
+        // within them is its offset less the wave's rows
+        const uint32_t loff = off - (uint32_t)(wave * RPI * row_bytes);
+#pragma unroll
+        for (int m = 0; m < Tl::LOADS; ++m) {
+          const int rr = m * NW * RPI + wave * RPI;  // first tile row of instruction m
+          const unsigned char* rb = base + (rr < 32 ? pg0 : pg1) * page_bytes +
+                                    (int64_t)((rr < 32 ? r0 : r1) + (rr & 31)) * row_bytes;
+          buffer_load_lds16(make_rsrc(rb, (uint32_t)(RPI * row_bytes)), smem + lds_w + m * NW * 1024, loff, 0u);
+        }
+      } else {
+        const uint32_t chunk_off = off - (uint32_t)(row0 * row_bytes);
+#pragma unroll
+        for (int m = 0; m < Tl::LOADS; ++m) {
+          const int kr = min(row0 + m * NW * RPI, Tk - 1 - key0);  // tile row, clamped to the last key
+          const unsigned char* rb = base + (kr < 32 ? pg0 : pg1) * page_bytes +
+                                    (int64_t)((kr < 32 ? r0 : r1) + (kr & 31)) * row_bytes;
+          global_load_lds16(rb + chunk_off, smem + lds_w + m * NW * 1024);
+        }
+      }
+      return;
+    }
     if (tile * PF_BN + PF_BN <= Tk) {
       // buffer loads: the tile's base in a scalar descriptor, the lane offset
       // in one 32-bit VGPR, the instruction's row step as a scalar offset (no
@@ -206,8 +246,8 @@ prefill_kernel(PrefillParams p) {
       }
     }
   };
-  auto load_k = [&](int tile, int buf) { load_tile(kbase, krow_bytes, koff, buf * TB, tile); };
-  auto load_v = [&](int tile, int buf) { load_tile(vbase, vrow_bytes, voff, (2 + buf) * TB, tile); };
+  auto load_k = [&](int tile, int buf) { load_tile(kbase, krow_bytes, kpage_bytes, koff, buf * TB, tile); };
+  auto load_v = [&](int tile, int buf) { load_tile(vbase, vrow_bytes, vpage_bytes, voff, (2 + buf) * TB, tile); };
   // this lane's query row: column r32 of this wave's 32 rows.  Row R of the
   // workgroup is head R % G at position q0 + R / G: the G heads of a position
   // sit in adjacent lanes, so a wave's rows span 32 / G positions and their
@@ -652,6 +692,11 @@ template <int D, typename T, int NW>
 static hipError_t launch_prefill_nw(const PrefillParams& p, bool causal, bool fuse, hipStream_t st) {
   dim3 grid((unsigned)(p.nqb * p.B * p.Hkv));
   dim3 block(64 * NW);
+  if (p.bt) {  // paged pools: the fused-Q instance (its norm and rotation are skipped when not given)
+    if (causal) hipLaunchKernelGGL((prefill_kernel<D, T, true, true, NW, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((prefill_kernel<D, T, false, true, NW, true>), grid, block, 0, st, p);
+    return hipGetLastError();
+  }
   if (causal) {
     if (fuse) hipLaunchKernelGGL((prefill_kernel<D, T, true, true, NW>), grid, block, 0, st, p);
     else hipLaunchKernelGGL((prefill_kernel<D, T, true, false, NW>), grid, block, 0, st, p);
@@ -676,16 +721,13 @@ static hipError_t launch_prefill(const PrefillParams& p, int nw, bool causal, bo
 
 using namespace nq;
 
-extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
-                                   const int64_t* k_strides, const void* v,
-                                   const int64_t* v_strides, void* o, const int64_t* o_strides,
-                                   float* lse, const int32_t* key_lens, int B, int Hq, int Hkv, int S,
-                                   int T, int D,
-                                   int dtype, const float* q_weight, float eps,
-                                   const float* cos_tab, const float* sin_tab, int max_pos,
-                                   const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
-                                   int causal, float sm_scale, void* stream) {
-  nq_clear_error();
+// Shared by the dense and paged entry points: bt == NULL for dense K/V.
+static int prefill_entry(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides, const int32_t* bt, int64_t bts, int page,
+                         void* o, const int64_t* o_strides, float* lse, const int32_t* key_lens, int B, int Hq,
+                         int Hkv, int S, int T, int D, int dtype, const float* q_weight, float eps,
+                         const float* cos_tab, const float* sin_tab, int max_pos, const int32_t* q_pos,
+                         const int32_t* q_pos_base, int q_pos0, int causal, float sm_scale, void* stream) {
   if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || T <= 0)
@@ -723,6 +765,7 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   p.q_pos = q_pos; p.q_pos_base = q_pos_base; p.q_pos0 = q_pos0;
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
   p.kv_lens = key_lens; p.kv_extra = 0; p.kv_max = T;
+  p.bt = bt; p.bts = bts; p.page = page;
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
   const bool fuse = q_weight != nullptr || cos_tab != nullptr;
@@ -742,4 +785,40 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
   const hipError_t e =
       with_head_dim(D, [&](auto dc) { return launch_prefill<decltype(dc)::value, bf16>(p, nw, causal, fuse, st); });
   return nq_check_launch(e);
+}
+
+extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                   const int64_t* k_strides, const void* v,
+                                   const int64_t* v_strides, void* o, const int64_t* o_strides,
+                                   float* lse, const int32_t* key_lens, int B, int Hq, int Hkv, int S,
+                                   int T, int D,
+                                   int dtype, const float* q_weight, float eps,
+                                   const float* cos_tab, const float* sin_tab, int max_pos,
+                                   const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
+                                   int causal, float sm_scale, void* stream) {
+  nq_clear_error();
+  return prefill_entry(q, q_strides, k, k_strides, v, v_strides, nullptr, 0, 0, o, o_strides, lse, key_lens, B,
+                       Hq, Hkv, S, T, D, dtype, q_weight, eps, cos_tab, sin_tab, max_pos, q_pos, q_pos_base,
+                       q_pos0, causal, sm_scale, stream);
+}
+
+extern "C" int nq_attn_prefill_paged_fwd(const void* q, const int64_t* q_strides, const void* k_pool,
+                                         const int64_t* k_pool_strides, const void* v_pool,
+                                         const int64_t* v_pool_strides, const int32_t* block_table,
+                                         int64_t bt_stride, int page_size, void* o,
+                                         const int64_t* o_strides, float* lse, int B, int Hq, int Hkv,
+                                         int S, int T, int D, int dtype, const float* q_weight,
+                                         float eps, const float* cos_tab, const float* sin_tab,
+                                         int max_pos, const int32_t* q_pos, const int32_t* q_pos_base,
+                                         int q_pos0, int causal, float sm_scale, void* stream) {
+  nq_clear_error();
+  if (!block_table) return nq_fail(NQ_ERR_INVALID, "a paged prefill needs the block table");
+  if (page_size <= 0 || page_size % 32)
+    return nq_fail(NQ_ERR_UNSUPPORTED, "page_size must be a positive multiple of 32, got %d", page_size);
+  if (T > 0 && bt_stride < (T + page_size - 1) / page_size)
+    return nq_fail(NQ_ERR_INVALID, "bt_stride %lld holds fewer than the %d pages of T %d", (long long)bt_stride,
+                   (T + page_size - 1) / page_size, T);
+  return prefill_entry(q, q_strides, k_pool, k_pool_strides, v_pool, v_pool_strides, block_table, bt_stride,
+                       page_size, o, o_strides, lse, nullptr, B, Hq, Hkv, S, T, D, dtype, q_weight, eps, cos_tab,
+                       sin_tab, max_pos, q_pos, q_pos_base, q_pos0, causal, sm_scale, stream);
 }

@@ -25,6 +25,7 @@ __all__ = [
     "KernelCall",
     "qk_norm_rope",
     "attention_prefill",
+    "attention_prefill_paged",
     "attention_decode",
     "attention_decode_paged",
     "kv_append_paged",
@@ -319,6 +320,61 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
     call = KernelCall(_lib.load().nq_attn_prefill_fwd, args, len(args) - 1, "nq_attn_prefill_fwd",
                       (q, k, v, cos_t, sin_t, pos, pb, qw, kl), (out, lse) if return_lse else out)
+    return call if plan else call.launch()
+
+
+def attention_prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                            block_table: torch.Tensor, *, T: int,
+                            q_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                            cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                            position_ids: Optional[torch.Tensor] = None, pos_offset: int = 0,
+                            pos_base: Optional[torch.Tensor] = None,
+                            causal: bool = True, sm_scale: Optional[float] = None,
+                            out: Optional[torch.Tensor] = None, return_lse: bool = False,
+                            plan: bool = False):
+    """``attention_prefill`` with K/V read from paged pools through the block table.
+
+    q: (B, Hq, S, D) pre-norm queries of a chunk; k_pool/v_pool:
+    (pages, Hkv, page_size, D) holding every sequence's T keys (K-hat and V,
+    the chunk's own rows already appended); block_table: (B, pages per
+    sequence).  ``causal`` keeps key j for query i iff j <= i + T - S.  This is
+    the continuation of a prompt into a ``PagedKVCache`` without a dense copy
+    of its pages (the reference concatenates, model/attention.py:31-38).
+    """
+    _require_device(q, k_pool, v_pool, block_table, out)
+    B, Hq, S, D = q.shape
+    for name, pool in (("k_pool", k_pool), ("v_pool", v_pool)):
+        _pool_check(pool, name)
+    if k_pool.shape != v_pool.shape or k_pool.shape[3] != D:
+        raise ValueError(f"pools {tuple(k_pool.shape)} / {tuple(v_pool.shape)} do not match q {tuple(q.shape)}")
+    if q.dtype != k_pool.dtype or q.dtype != v_pool.dtype:
+        raise TypeError("q and the pools must share one dtype")
+    Hkv, P = k_pool.shape[1], k_pool.shape[2]
+    bt = _block_table(block_table, B, q.device)
+    if not 0 < T <= bt.shape[1] * P:
+        raise ValueError(f"T={T} must be in [1, {bt.shape[1] * P}] (block-table pages x page_size)")
+    dt = _code(q)
+    q = _rows_in(q)
+    if out is None:
+        out = torch.empty(B, S, Hq, D, dtype=q.dtype, device=q.device).transpose(1, 2)
+    elif tuple(out.shape) != (B, Hq, S, D) or out.dtype != q.dtype:
+        raise ValueError(f"out must be (B, Hq, S, D) = {(B, Hq, S, D)} in {q.dtype}")
+    _rows_out(out, "out")
+    lse = torch.empty(B, Hq, S, dtype=torch.float32, device=q.device) if return_lse else None
+    dev = q.device
+    cos_t, sin_t, max_pos = _tables(cos, sin, dev)
+    pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
+    pb = _i32(pos_base, dev)
+    qw = _f32(q_weight, dev)
+    st = _lib.strides3
+    args = (
+        _ptr(q), st(q.stride()[:3]), _ptr(k_pool), st(k_pool.stride()[:3]), _ptr(v_pool),
+        st(v_pool.stride()[:3]), _ptr(bt), bt.stride(0), P, _ptr(out), st(out.stride()[:3]), _ptr(lse),
+        B, Hq, Hkv, S, int(T), D, dt, _ptr(qw), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
+        _ptr(pos), _ptr(pb), int(pos_offset), int(bool(causal)),
+        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    call = KernelCall(_lib.load().nq_attn_prefill_paged_fwd, args, len(args) - 1, "nq_attn_prefill_paged_fwd",
+                      (q, k_pool, v_pool, bt, cos_t, sin_t, pos, pb, qw), (out, lse) if return_lse else out)
     return call if plan else call.launch()
 
 

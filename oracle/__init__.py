@@ -17,6 +17,7 @@ from .attention_oracle import (  # noqa: F401
     attention_path,
     reference_path_sdpa,
     reference_decode_sdpa,
+    reference_chunk_sdpa,
     decode_path,
     attention_module_forward,
     OracleKVCache,

@@ -325,6 +325,39 @@ def reference_decode_sdpa(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Ten
     return F.scaled_dot_product_attention(q, k, v), k_all, v_all
 
 
+def reference_chunk_sdpa(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+                         q_weight: Optional[torch.Tensor], k_weight: Optional[torch.Tensor],
+                         eps: float, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """A prompt continuation in the reference's composition, as the CPU baseline
+    times it: the chunk's S new tokens sit at positions T0 .. T0+S-1 (T0 =
+    k_cache.shape[2], the rows already cached as K-hat and V); QK-Norm and RoPE
+    of the chunk's q and k (attention.py:95-100), KVCache.update's
+    concatenation (attention.py:35-44), ``repeat_interleave``
+    (attention.py:105-108) and SDPA (attention.py:110-115) with the
+    bottom-right causal mask of true positions (the reference passes none with
+    a cache, quirk Q8; the build's chunked prefill is causal).  Pinned against
+    ``attention_path`` in the oracle tests.
+    """
+    import torch.nn.functional as F
+    T0, S = k_cache.shape[2], q.shape[2]
+    pos = torch.arange(T0, T0 + S)
+    if q_weight is not None:
+        q = rms_norm(q, q_weight, eps)
+    if k_weight is not None:
+        k_new = rms_norm(k_new, k_weight, eps)
+    c, s_ = _gather_table(cos, pos), _gather_table(sin, pos)
+    q, k_new = rotate_half(q, c, s_), rotate_half(k_new, c, s_)
+    k = torch.cat([k_cache, k_new], dim=2)
+    v = torch.cat([v_cache, v_new], dim=2)
+    G = q.shape[1] // k.shape[1]
+    if G > 1:
+        k = k.repeat_interleave(G, dim=1)
+        v = v.repeat_interleave(G, dim=1)
+    keep = torch.ones(S, T0 + S, dtype=torch.bool).tril(T0)
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=keep)
+
+
 def decode_path(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 lens: torch.Tensor, *, q_weight: Optional[torch.Tensor], eps: float,
                 cos: torch.Tensor, sin: torch.Tensor, q_pos: torch.Tensor,

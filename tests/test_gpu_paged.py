@@ -16,7 +16,7 @@ import torch
 
 import nano_qwen_amd as nq
 from nano_qwen_amd import ops
-from oracle import decode_path, rms_norm, rope_tables, rotate_half
+from oracle import attention, decode_path, rms_norm, rope_tables, rotate_half
 from tests.helpers import assert_bf16_close, assert_close_for, randn, say
 
 pytestmark = pytest.mark.gpu
@@ -341,3 +341,52 @@ def test_fused_append_paged_full_size():
         ref = _oracle_append(q[b:b + 1], kn[b:b + 1], vn[b:b + 1], kd[None], vd[None], held[b:b + 1],
                              qw, kw, cos, sin, held[b:b + 1])
         assert_bf16_close(o[b:b + 1], ref, f"fused append paged b={b} len={L}")
+
+
+def test_paged_chunked_prefill_full_size():
+    """An 8B-like sequence set (B4 x 8192, 32/8 heads, D128) prefilled in four
+    2048-token chunks into 64-row pages dealt in a seeded random order (unused
+    pages NaN): each chunk appends its K-hat/V (norm and rotation fused) and its
+    queries attend all keys so far through the block table.  Every chunk's
+    output is bit-identical to the dense prefill over the same K-hat/V, and
+    sampled query blocks match the oracle."""
+    say("paged chunked prefill B4 x 8192 32/8 D128, 4 chunks of 2048, P64")
+    B, Hq, Hkv, D, T, C, P = 4, 32, 8, 128, 8192, 2048, 64
+    q = randn(B, T, Hq, D, seed=5101, dtype=torch.bfloat16).transpose(1, 2)
+    k = randn(B, T, Hkv, D, seed=5102, dtype=torch.bfloat16).transpose(1, 2)
+    v = randn(B, T, Hkv, D, seed=5103, dtype=torch.bfloat16).transpose(1, 2)
+    qw = 1 + 0.02 * randn(D, seed=5104)
+    kw = 1 + 0.02 * randn(D, seed=5105)
+    cos, sin = rope_tables(D, T, 1e6)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    qwd, kwd, cd, sd = qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV)
+    # dense K-hat of the whole sequence (the row kernel), for the dense reference launches
+    khat = nq.qk_norm_rope(k=kd, k_weight=kwd, eps=1e-6, cos=cd, sin=sd)[1]
+    npg = T // P
+    total = B * npg + 5
+    perm = torch.randperm(total, generator=torch.Generator().manual_seed(5106)).to(torch.int32)
+    bt = perm[:B * npg].view(B, npg).to(DEV)
+    kp = torch.full((total, Hkv, P, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    vp = torch.full_like(kp, float("nan"))
+    outs = []
+    for c in range(T // C):
+        p0 = c * C
+        ops.kv_append_paged(kd[:, :, p0:p0 + C], vd[:, :, p0:p0 + C], kp, vp, bt, k_weight=kwd, eps=1e-6,
+                            cos=cd, sin=sd, row_offset=p0, pos_offset=p0)
+        got = ops.attention_prefill_paged(qd[:, :, p0:p0 + C], kp, vp, bt, T=p0 + C, q_weight=qwd, eps=1e-6,
+                                          cos=cd, sin=sd, causal=True, pos_offset=p0)
+        want = ops.attention_prefill(qd[:, :, p0:p0 + C], khat[:, :, :p0 + C], vd[:, :, :p0 + C], q_weight=qwd,
+                                     eps=1e-6, cos=cd, sin=sd, causal=True, pos_offset=p0)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all(), f"chunk {c}"
+        assert torch.equal(got, want), f"chunk {c}: paged differs from dense (max {float((got.float() - want.float()).abs().max()):.3e})"
+        outs.append(got.float().cpu())
+    # oracle on sampled 64-row query blocks (first chunk's first block, last chunk's first and last)
+    kf = rms_norm(k.float(), kw, 1e-6)
+    kh = rotate_half(kf, cos[None, None], sin[None, None])
+    for c, s0 in ((0, 0), (3, 0), (3, C - 64)):
+        p0 = c * C
+        rows = torch.arange(p0 + s0, p0 + s0 + 64)
+        qh = rotate_half(rms_norm(q[:, :, rows].float(), qw, 1e-6), cos[rows][None, None], sin[rows][None, None])
+        ref = attention(qh, kh[:, :, :p0 + C], v[:, :, :p0 + C].float(), causal=True, causal_offset=p0 + s0)
+        assert_bf16_close(outs[c][:, :, s0:s0 + 64], ref, f"chunk {c} rows {s0}..{s0 + 63} vs oracle")

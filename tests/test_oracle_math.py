@@ -12,7 +12,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle import (attention, attention_path, decode_path, reference_decode_sdpa, reference_path_sdpa,
+from oracle import (attention, attention_path, decode_path, reference_chunk_sdpa, reference_decode_sdpa,
+                    reference_path_sdpa,
                     rms_norm, rope_inv_freq, rope_tables, rotate_half, yarn_correction_range,
                     yarn_inv_freq)
 
@@ -280,3 +281,27 @@ def test_reference_decode_sdpa_equals_decode_path():
     og, _, _ = reference_decode_sdpa(q, kn, vn, kc, vc, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos,
                                      sin=sin, repeat_kv=False)
     torch.testing.assert_close(og, o, rtol=1e-12, atol=1e-12)
+
+
+def test_reference_chunk_sdpa_equals_attention_path():
+    """The chunked-prefill CPU baseline (norm + RoPE of the chunk, concatenation after the
+    cached K-hat, repeat_interleave, SDPA with the bottom-right mask) equals attention_path
+    over the whole sequence at the chunk's rows; a top-left mask (a plausible slip) does not."""
+    Hq, Hkv, D, T0, S = 8, 2, 32, 19, 7
+    q = _rand(1, Hq, T0 + S, D, seed=81)
+    k, v = _rand(1, Hkv, T0 + S, D, seed=82), _rand(1, Hkv, T0 + S, D, seed=83)
+    qw, kw = 1 + 0.1 * _rand(D, seed=84), 1 + 0.1 * _rand(D, seed=85)
+    cos, sin = rope_tables(D, 64, 1e6)
+    cos, sin = cos.double(), sin.double()
+    full, kh = attention_path(q, k, v, q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin,
+                              q_pos=torch.arange(T0 + S), causal=True, compute_dtype=torch.float64,
+                              return_khat=True)
+    o = reference_chunk_sdpa(q[:, :, T0:], k[:, :, T0:], v[:, :, T0:], kh[:, :, :T0], v[:, :, :T0],
+                             q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin)
+    torch.testing.assert_close(o, full[:, :, T0:], rtol=1e-5, atol=1e-6)
+    kw_args = dict(q_weight=qw, k_weight=kw, eps=1e-6, cos=cos, sin=sin, q_pos=torch.arange(T0, T0 + S),
+                   k_pos=torch.arange(T0 + S), causal=True, compute_dtype=torch.float64)
+    br = attention_path(q[:, :, T0:], k, v, causal_offset=T0, **kw_args)  # bottom-right frontier
+    torch.testing.assert_close(o, br, rtol=1e-5, atol=1e-6)
+    tl = attention_path(q[:, :, T0:], k, v, causal_offset=0, **kw_args)  # top-left frontier
+    assert not torch.allclose(tl, o, rtol=1e-3, atol=1e-3)
