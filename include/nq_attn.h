@@ -137,6 +137,30 @@ int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, const void* k,
                         int causal, float sm_scale, void* stream);
 
 /*
+ * nq_attn_prefill_fwd with a general attention mask as an additive bias.
+ *
+ * Replaces SDPA's attn_mask at model/attention.py:110-113 (passed by callers
+ * such as training/reward_model.py:45): a bool keep-mask (True = attend) is
+ * given as 0 / -inf, a float mask as its values, both in `dtype`.
+ * bias[b, h, i, j] lies at bias + b * bias_strides[0] + h * bias_strides[1] +
+ * i * bias_strides[2] + j (element strides; 0 broadcasts an axis); every
+ * row's keys are contiguous and readable up to T rounded up to a multiple of
+ * 8; the base is 16-byte aligned and the strides are non-negative multiples
+ * of 8.  The bias adds to scale * q.k before the softmax; key_lens and causal
+ * still apply.  A row whose keys are all masked gets zeros and LSE -inf (as
+ * SDPA gives).  Requires 128 % (Hq / Hkv) == 0.  Other arguments as
+ * nq_attn_prefill_fwd.
+ */
+int nq_attn_prefill_bias_fwd(const void* q, const int64_t* q_strides, const void* k,
+                             const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                             void* o, const int64_t* o_strides, float* lse, const int32_t* key_lens,
+                             const void* bias, const int64_t* bias_strides, int B, int Hq, int Hkv,
+                             int S, int T, int D, int dtype, const float* q_weight, float eps,
+                             const float* cos_tab, const float* sin_tab, int max_pos,
+                             const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0, int causal,
+                             float sm_scale, void* stream);
+
+/*
  * nq_attn_prefill_fwd over K/V held in paged pools: a chunk of S new queries
  * attends the T keys of its sequence (the T - S already cached plus the S just
  * appended), read through the block table, so a chunked prefill into a paged
@@ -343,18 +367,48 @@ int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const in
                 int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream);
 
 /*
+ * nq_attn_bwd of a forward that ran with an attention bias
+ * (nq_attn_prefill_bias_fwd): bias as there, plus its transpose bias_t
+ * (bias_t[b, h, j, i] at bias_t + b * bias_t_strides[0] +
+ * h * bias_t_strides[1] + j * bias_t_strides[2] + i, each key's queries
+ * contiguous and readable up to S rounded up to 8; same alignment rules),
+ * which the dK/dV kernel reads.  lse is the bias forward's (-inf rows get
+ * zero gradients).  Other arguments as nq_attn_bwd.
+ */
+int nq_attn_bwd_bias(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                     const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
+                     const void* dout, const int64_t* do_strides, const float* lse,
+                     const int32_t* key_lens, const void* bias, const int64_t* bias_strides,
+                     const void* bias_t, const int64_t* bias_t_strides, void* dq,
+                     const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                     const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
+                     int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale,
+                     void* stream);
+
+/*
+ * Bytes of fp32 workspace nq_qk_norm_rope_bwd needs when it forms the weight
+ * gradient: one partial sum of D values per block of its grid.
+ */
+int64_t nq_qk_norm_rope_bwd_workspace_bytes(int B, int S, int H, int D);
+
+/*
  * Backward of QK-Norm + RoPE (model/norm.py:17-22 and model/rope.py:133-161
  * as applied at attention.py:95-100): given the pre-norm rows x and the
- * gradient dy of y = rope(rmsnorm(x) * weight), writes dx and ADDS the weight
- * gradient into dweight (fp32, D elements; the caller zeroes it).  weight /
- * dweight NULL: no norm; cos_tab NULL: no rotation.  Positions as in
- * nq_qk_norm_rope.  x, dy, dx: (B, H, S, D) with strides {batch, head, seq}.
+ * gradient dy of y = rope(rmsnorm(x) * weight), writes dx and the weight
+ * gradient dweight (fp32, D elements, fully written).  The blocks store
+ * partial sums of dweight in the workspace
+ * (nq_qk_norm_rope_bwd_workspace_bytes), which a second launch adds in block
+ * order: dweight is the same bit for bit on every run.  weight / dweight
+ * NULL: no norm (workspace unused); cos_tab NULL: no rotation.  Positions as
+ * in nq_qk_norm_rope.  x, dy, dx: (B, H, S, D) with strides {batch, head,
+ * seq}.
  */
 int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, const void* dy,
                         const int64_t* dy_strides, void* dx, const int64_t* dx_strides,
-                        const float* weight, float* dweight, int B, int S, int H, int D, int dtype,
-                        float eps, const float* cos_tab, const float* sin_tab, int max_pos,
-                        const int32_t* pos, const int32_t* pos_base, int pos0, void* stream);
+                        const float* weight, float* dweight, void* workspace, int64_t workspace_bytes,
+                        int B, int S, int H, int D, int dtype, float eps, const float* cos_tab,
+                        const float* sin_tab, int max_pos, const int32_t* pos, const int32_t* pos_base,
+                        int pos0, void* stream);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,16 @@ SIGNATURES = {
         _p, _p, _i32,                                # q_pos, q_pos_base, q_pos0
         _i32, _f32, _p,                              # causal, sm_scale, stream
     ]),
+    "nq_attn_prefill_bias_fwd": (_i32, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,  # q, k, v, o (+ strides)
+        _p, _p,                                      # lse, key_lens
+        _p, _i64p,                                   # bias, bias_strides
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype
+        _p, _f32,                                    # q_weight, eps
+        _p, _p, _i32,                                # cos, sin, max_pos
+        _p, _p, _i32,                                # q_pos, q_pos_base, q_pos0
+        _i32, _f32, _p,                              # causal, sm_scale, stream
+    ]),
     "nq_attn_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "nq_attn_decode_fwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p,             # q, k_cache, v_cache (+ strides)
@@ -130,9 +140,19 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype
         _i32, _f32, _p,                              # causal, sm_scale, stream
     ]),
+    "nq_attn_bwd_bias": (_i32, [
+        _p, _i64p, _p, _i64p, _p, _i64p,             # q, k, v (+ strides)
+        _p, _i64p, _p, _i64p, _p, _p,                # o, dout (+ strides), lse, key_lens
+        _p, _i64p, _p, _i64p,                        # bias, bias_strides, bias_t, bias_t_strides
+        _p, _i64p, _p, _i64p, _p, _i64p,             # dq, dk, dv (+ strides)
+        _p, _i64,                                    # workspace, workspace_bytes
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32,    # B, Hq, Hkv, S, T, D, dtype
+        _i32, _f32, _p,                              # causal, sm_scale, stream
+    ]),
+    "nq_qk_norm_rope_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "nq_qk_norm_rope_bwd": (_i32, [
         _p, _i64p, _p, _i64p, _p, _i64p,             # x, dy, dx (+ strides)
-        _p, _p,                                      # weight, dweight
+        _p, _p, _p, _i64,                            # weight, dweight, workspace, workspace_bytes
         _i32, _i32, _i32, _i32, _i32,                # B, S, H, D, dtype
         _f32, _p, _p, _i32,                          # eps, cos, sin, max_pos
         _p, _p, _i32,                                # pos, pos_base, pos0

@@ -8,22 +8,22 @@ attention_mask=None, kv_cache=None)`` signature.  ``KVCache`` keeps
 (B, Hkv, T, D) layout, but stores rows in a preallocated buffer instead of
 concatenating on every step.
 
-Dispatch (following kernels/flash_attn.py:139's convention):
-  * device tensors, no attention_mask, no autograd -> gfx950 kernels:
-    one row-kernel launch (K-Norm + RoPE -> K-hat, plus the V copy when a
-    cache is used), then the prefill kernel (Q-Norm + RoPE fused into the Q
-    load), or the split-K decode kernel when a cache is present and S == 1;
-  * autograd (training, no cache) -> the same kernels through an autograd
-    Function whose backward is the FlashAttention-2 backward kernels plus the
-    QK-Norm + RoPE backward kernel (nano_qwen_amd.autograd);
-  * an attention_mask that is a key-padding mask (keeps, for every head and
-    query, the same prefix [0, L_b) of each sequence's keys: a bool or 0/-inf
-    float mask of shape (B or 1, 1, 1, T), (1, T) or (T,), as a right-padded
-    batch gives) and no cache -> the same kernels with per-sequence key
-    counts, non-causal as SDPA is with a mask (attention.py:113), forward and
-    backward;
-  * any other attention_mask, attention dropout, or autograd with a cache
-    -> torch ops on the device, the reference's own arithmetic (SDPA);
+Every forward runs on the gfx950 kernels; there is no second backend:
+  * no attention_mask, no autograd: one row-kernel launch (K-Norm + RoPE ->
+    K-hat, plus the V copy when a cache is used), then the prefill kernel
+    (Q-Norm + RoPE fused into the Q load), or the split-K decode kernel when
+    a cache is present and S == 1;
+  * autograd (training, with or without a plain KVCache): the same kernels
+    through an autograd Function whose backward is the FlashAttention-2
+    backward kernels plus the QK-Norm + RoPE backward kernel
+    (nano_qwen_amd.autograd);
+  * an attention_mask, non-causal as SDPA is with a mask (attention.py:113):
+    a key-padding mask (the same prefix [0, L_b) of each sequence's keys for
+    every head and query, as a right-padded batch gives) as per-sequence key
+    counts; any other bool or float mask as an additive bias the kernels read
+    per tile (``ops.AttnBias``), forward and backward;
+  * attention dropout while training -> NotImplementedError (no reference
+    config sets it; the kernels have no dropout);
   * host tensors -> RuntimeError (the kernels are the product; there is no
     CPU path).
 
@@ -43,14 +43,15 @@ from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import autograd, ops
 from .config import num_kv_groups
 from .norm import RMSNorm
 from .rope import RotaryEmbedding
 
-# Counters of which path forward() took (kernel launches vs torch fallback).
+# Counters of which path forward() took.  "torch_forward" counts forwards
+# that left the kernels; no path does, so it stays 0 (kept for callers that
+# read it).
 stats = {"kernel_forward": 0, "kernel_train_forward": 0, "torch_forward": 0}
 
 
@@ -413,37 +414,61 @@ class Attention(nn.Module):
             # no query rows: the reference's SDPA returns an empty output and its
             # cache update appends nothing (attention.py:103-118); no launch here
             return self.o_proj(q.new_zeros(B, S, H * D))
-        dropout = self.training and getattr(self.config, "attention_dropout", 0.0) > 0
+        if self.training and getattr(self.config, "attention_dropout", 0.0) > 0:
+            # attention.py:114 applies dropout_p while training; no reference
+            # config sets attention_dropout above 0, and the kernels have no
+            # dropout
+            raise NotImplementedError(
+                f"attention_dropout={self.config.attention_dropout} while training: the HIP attention "
+                "kernels implement no dropout; set config.attention_dropout = 0.0 (every reference "
+                "config does) or evaluate with model.eval()")
         qw = self.q_norm.weight if self.qk_norm else None
         kw = self.k_norm.weight if self.qk_norm else None
         needs_grad = torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (q, k, v, qw, kw))
-        key_lens = None
-        if attention_mask is not None and kv_cache is None and not dropout:
-            key_lens = key_padding_lengths(attention_mask, B, S)
-        if (attention_mask is not None and key_lens is None) or dropout or (needs_grad and kv_cache is not None):
-            stats["torch_forward"] += 1
-            return self._torch_forward(q, k, v, position_ids, attention_mask, kv_cache)
-        causal = key_lens is None  # SDPA is not causal once a mask is given
+        paged = isinstance(kv_cache, PagedKVCache)
+        ragged = kv_cache is not None and not paged and kv_cache.lens is not None
+        if (paged or ragged) and (attention_mask is not None or needs_grad):
+            raise NotImplementedError("ragged and paged caches take no attention mask and no autograd "
+                                      "(serving caches); use a plain KVCache or none")
+        past = kv_cache.seq_len if (kv_cache is not None and not paged) else 0
+        T = past + S
+        # attention.py:110-113: SDPA takes the mask as given.  A mask that keeps
+        # the same prefix of each sequence's keys for every head and query runs
+        # as per-sequence key counts; any other as an additive bias read by the
+        # kernels, per tile.
+        key_lens, bias = None, None
+        if attention_mask is not None:
+            key_lens = key_padding_lengths(attention_mask, B, T)
+            if key_lens is None:
+                bias = ops.AttnBias(attention_mask, B, H, S, T, q.dtype, q.device, transpose=needs_grad)
+        # is_causal only without a mask and a cache (attention.py:113), or for
+        # a multi-token step into a cache under the fixed semantics
+        causal = attention_mask is None and (kv_cache is None or (self.cache_prefill_causal and S > 1))
 
         q4 = q.view(B, S, H, D).transpose(1, 2)
         k4 = k.view(B, S, Hkv, D).transpose(1, 2)
         v4 = v.view(B, S, Hkv, D).transpose(1, 2)
         cos, sin = self.rotary_emb.tables_f32()
         eps = self.config.rms_norm_eps
+        pos_offset = past if (self.rope_positions == "cache" and position_ids is None) else 0
         if needs_grad:
-            # training: the forward and backward both on the kernels (causal,
-            # no cache: attention.py:113 with kv_cache None)
+            # training: the forward and backward both on the kernels; with a
+            # cache the new rows are appended and every cached row attended
             stats["kernel_train_forward"] += 1
+            kv_store = None
+            if kv_cache is not None:
+                kv_cache.reserve(B, Hkv, T, D, k.dtype, k.device)
+                kc, vc = kv_cache.storage()
+                kv_store = (kc, vc, past)
+                kv_cache.advance(S)
             o = autograd.attention_core(q4, k4, v4, qw, kw, cos=cos, sin=sin,
-                                        position_ids=position_ids, eps=eps, causal=causal,
-                                        key_lens=key_lens)
+                                        position_ids=position_ids, pos_offset=pos_offset, eps=eps,
+                                        causal=causal, key_lens=key_lens, bias=bias, kv_store=kv_store)
             return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
         stats["kernel_forward"] += 1
-        if isinstance(kv_cache, PagedKVCache):
+        if paged:
             return self._paged_forward(q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps)
-        past = kv_cache.seq_len if kv_cache is not None else 0
-        pos_offset = past if (self.rope_positions == "cache" and position_ids is None) else 0
 
         if kv_cache is None:
             k_hat = torch.empty(B, S, Hkv, D, dtype=k.dtype, device=k.device).transpose(1, 2)
@@ -451,14 +476,14 @@ class Attention(nn.Module):
                              position_ids=position_ids, pos_offset=pos_offset)
             o = ops.attention_prefill(q4, k_hat, v4, q_weight=qw, eps=eps, cos=cos, sin=sin,
                                       position_ids=position_ids, pos_offset=pos_offset, causal=causal,
-                                      key_lens=key_lens)
+                                      key_lens=key_lens, bias=bias)
             return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
 
-        if kv_cache.lens is not None:
+        if ragged:
             return self._ragged_decode(q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps)
         kv_cache.reserve(B, Hkv, past + S, D, k.dtype, k.device)
         kc, vc = kv_cache.storage()
-        if S == 1:
+        if S == 1 and attention_mask is None:
             # one launch pair: the new K-hat/V row is built, written to row
             # `past` and attended inside the decode kernel (the storage is a
             # pool of B pages of `capacity` rows); positions as the row kernel
@@ -473,10 +498,9 @@ class Attention(nn.Module):
         ops.qk_norm_rope(k=k4, v=v4, k_out=kc, v_out=vc, k_weight=kw, eps=eps, cos=cos, sin=sin,
                          position_ids=position_ids, pos_offset=pos_offset, kv_row_offset=past)
         kv_cache.advance(S)
-        T = past + S
         o = ops.attention_prefill(q4, kc[:, :, :T], vc[:, :, :T], q_weight=qw, eps=eps, cos=cos,
                                   sin=sin, position_ids=position_ids, pos_offset=pos_offset,
-                                  causal=self.cache_prefill_causal)
+                                  causal=causal, key_lens=key_lens, bias=bias)
         return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
 
     def _ragged_decode(self, q4, k4, v4, position_ids, kv_cache, cos, sin, qw, kw, eps):
@@ -539,56 +563,3 @@ class Attention(nn.Module):
         cache.lens.add_(S)
         cache.host_lens = new
         return self.o_proj(o.transpose(1, 2).reshape(B, S, H * D))
-
-    # ------------------------------------------------------------- torch path
-    def _torch_forward(self, q, k, v, position_ids, attention_mask, kv_cache):
-        """The reference's own arithmetic (attention.py:91-118) for autograd / masks."""
-        if isinstance(kv_cache, PagedKVCache) or (kv_cache is not None and kv_cache.lens is not None):
-            raise NotImplementedError("ragged and paged caches run on the kernel path only (no mask, no autograd)")
-        B, S, _ = q.shape
-        H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
-        q = q.view(B, S, H, D).transpose(1, 2)
-        k = k.view(B, S, Hkv, D).transpose(1, 2)
-        v = v.view(B, S, Hkv, D).transpose(1, 2)
-        if self.qk_norm:
-            q = _rms(q, self.q_norm.weight, self.config.rms_norm_eps)
-            k = _rms(k, self.k_norm.weight, self.config.rms_norm_eps)
-        past = kv_cache.seq_len if kv_cache is not None else 0
-        if position_ids is None and self.rope_positions == "cache" and past:
-            position_ids = torch.arange(past, past + S, device=q.device)[None].expand(B, S)
-        cos, sin = self.rotary_emb(q, position_ids)
-        q, k = _rotate(q, cos, sin), _rotate(k, cos, sin)
-        if kv_cache is not None:
-            k, v = kv_cache.update(k, v)
-        G = self.num_kv_groups
-        if G > 1:
-            k = k.repeat_interleave(G, dim=1)
-            v = v.repeat_interleave(G, dim=1)
-        causal = attention_mask is None and (kv_cache is None or (self.cache_prefill_causal and S > 1))
-        T = k.shape[2]
-        mask, is_causal = attention_mask, False
-        if causal and T == S:
-            is_causal = True
-        elif causal:
-            # bottom-right aligned causal mask for queries appended after T - S cached rows
-            mask = torch.ones(S, T, dtype=torch.bool, device=q.device).tril(diagonal=T - S)
-        o = F.scaled_dot_product_attention(
-            q, k, v, attn_mask=mask, is_causal=is_causal,
-            dropout_p=self.config.attention_dropout if self.training else 0.0)
-        o = o.transpose(1, 2).contiguous().view(B, S, -1)
-        return self.o_proj(o)
-
-
-def _rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).type_as(x) * w
-
-
-def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    half = x.shape[-1] // 2
-    if cos.dim() == 2:
-        cos, sin = cos[None, None], sin[None, None]
-    else:
-        cos, sin = cos[:, None], sin[:, None]
-    x1, x2 = x[..., :half], x[..., half:]
-    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)

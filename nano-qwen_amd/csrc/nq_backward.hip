@@ -128,7 +128,10 @@ __device__ __forceinline__ bf16x8 bw_tr8(const unsigned char* p) {
 }
 
 // ---------------------------------------------------------------- dQ
-template <int D, typename T, bool CAUSAL, int NW>
+// BIAS: the forward's additive bias (p.bias) enters every score (every tile
+// takes the masked path); a row the bias masks entirely has LSE -inf and
+// P = 0 (its scratch LSE is stored +inf for the dK/dV kernel).
+template <int D, typename T, bool CAUSAL, int NW, bool BIAS = false>
 __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
   using L = BwTile<D>;
   constexpr int NDB = D / 16, NDO = D / 32;
@@ -206,7 +209,8 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
     }
     dlt = xor32_sum(acc);
   }
-  const float lse2 = p.lse[((int64_t)b * p.Hq + head) * p.S + qi_c] * kLog2e;
+  float lse2 = p.lse[((int64_t)b * p.Hq + head) * p.S + qi_c] * kLog2e;
+  if (BIAS && !(lse2 > -INFINITY)) lse2 = INFINITY;  // no key kept: P = exp2(s - inf) = 0
   // the dK/dV kernel reads both per 32-row tile from the scratch; the
   // workgroup of the last q-block also zeroes its heads' slots past S (the
   // dK/dV kernel's masked rows then see finite values)
@@ -264,7 +268,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
     const uint32_t ka = lds_addr(Kt);  // the V tile is TB bytes on
     // a tile inside every row's bounds (all keys below T and at or before
     // the block's first query's frontier, no rows past S) skips the mask
-    const bool full = n0 + BW_BN <= Tk && q0 + p.BM <= p.S && (!CAUSAL || n0 + BW_BN - 1 <= q0 + p.coff);
+    const bool full = !BIAS && n0 + BW_BN <= Tk && q0 + p.BM <= p.S && (!CAUSAL || n0 + BW_BN - 1 <= q0 + p.coff);
     // the two 32-key blocks of the tile (kb a compile-time constant, so its
     // LDS offset goes into the read instructions)
     auto key_block = [&](auto KB) {
@@ -294,10 +298,19 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           floatx8 ds;
+          // the bias of the lane's 8 keys n0 + kb*32 + ks*16 + hh*8 + 0..7
+          bf16x8 bv{};
+          if constexpr (BIAS) {
+            const int k8 = n0 + kb * 32 + ks * 16 + hh * 8;
+            if (k8 < Tk)
+              bv = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.bias) + b * p.bsb +
+                                                    head * p.bsh + (int64_t)qi_c * p.bss + k8);
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int i = ks * 8 + e;
             float x = __builtin_fmaf(s[i], p.scale_log2, -lse2);
+            if constexpr (BIAS) x = __builtin_fmaf((float)bv[e], kLog2e, x);
             if constexpr (decltype(masked)::value) {
               // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
               const int key = n0 + kb * 32 + bw_cidx(i, hh);
@@ -340,7 +353,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) bwd_dq_kernel(BwdParams p) {
 
 // ---------------------------------------------------------------- dK, dV
 // D = 64 fits three workgroups per CU (168 VGPRs), D = 128 two
-template <int D, typename T, bool CAUSAL>
+template <int D, typename T, bool CAUSAL, bool BIAS = false>
 __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParams p) {
   using L = BwTile<D>;
   constexpr int NDB = D / 16, NDO = D / 32;
@@ -481,6 +494,8 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
   int gcur = 0, qnext = qtop;
   for (int it = 0; it < niter; ++it) {
     const int qt = qnext;  // this step's query tile
+    const int gstep = gcur;  // and head
+    (void)gstep;
     advance(gcur, qnext);
     wait_vmcnt0();  // the LSE / Delta rows always come through global_load_lds
     __syncthreads();
@@ -537,10 +552,18 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
           const int r0 = ks * 16 + hh * 8 + i4h * 4;
           const floatx4 lv = *reinterpret_cast<const floatx4*>(lse_t + r0);
           const floatx4 dv4 = *reinterpret_cast<const floatx4*>(dlt_t + r0);
+          // the transposed bias of this key for queries qt + r0 + 0..3
+          bf16x4 bv{};
+          if constexpr (BIAS) {
+            if (key < Tk && qt + r0 < p.S)
+              bv = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16*>(p.bias_t) + b * p.btsb +
+                                                    (kvh * p.G + gstep) * p.btsh + (int64_t)key * p.btss + qt + r0);
+          }
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int i = ks * 8 + i4h * 4 + u;
             float x = __builtin_fmaf(s[i], p.scale_log2, -lv[u]);
+            if constexpr (BIAS) x = __builtin_fmaf((float)bv[u], kLog2e, x);
             if constexpr (decltype(masked)::value) {
               // masked: exp2(-inf) = 0, selected before the exp (no branch around it)
               const int q = qt + r0 + u;
@@ -557,7 +580,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_dkdv_kernel(BwdParam
       }
     };
     const int kw1 = kw0 + 31;  // the wave's last key
-    if (kw1 < Tk && qt + BW_BQ <= p.S && (!CAUSAL || kw1 <= qt + p.coff))
+    if (!BIAS && kw1 < Tk && qt + BW_BQ <= p.S && (!CAUSAL || kw1 <= qt + p.coff))
       probs(std::false_type{});
     else
       probs(std::true_type{});
@@ -604,6 +627,17 @@ static hipError_t launch_bwd(const BwdParams& p, int nw, bool causal, hipStream_
   const dim3 gq((unsigned)(p.nqb * p.B * p.Hkv));
   const dim3 gk((unsigned)(((p.T + BW_KEYS - 1) / BW_KEYS) * p.B * p.Hkv));
   const dim3 bq(64 * nw);
+  if (p.bias) {  // 4-wave dQ workgroups
+    if (nw != 4) return hipErrorInvalidValue;
+    if (causal) {
+      hipLaunchKernelGGL((bwd_dq_kernel<D, T, true, 4, true>), gq, bq, 0, st, p);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, T, true, true>), gk, dim3(256), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_kernel<D, T, false, 4, true>), gq, bq, 0, st, p);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, T, false, true>), gk, dim3(256), 0, st, p);
+    }
+    return hipGetLastError();
+  }
   if (causal) {
     if (nw == 8) hipLaunchKernelGGL((bwd_dq_kernel<D, T, true, 8>), gq, bq, 0, st, p);
     else hipLaunchKernelGGL((bwd_dq_kernel<D, T, true, 4>), gq, bq, 0, st, p);
@@ -621,8 +655,9 @@ static hipError_t launch_bwd(const BwdParams& p, int nw, bool causal, hipStream_
 // rotation by -theta): dw += g * x * r (summed over rows), and with
 // u = g * w: dx = r * u - x * (r^3 / D) * sum(u * x).  Rows are held as in
 // the forward row kernel (D/16 lanes, a lane owns 8 elements and their
-// rotate-half partners).  dw is accumulated per block in LDS, then one atomic
-// add per block and element into the caller's zeroed fp32 buffer.
+// rotate-half partners).  dw is accumulated per block in LDS and each block
+// stores its partial sum in the workspace; a second launch adds the partials
+// in block order, so dw is the same bit for bit on every run (no atomics).
 struct NormBwdParams {
   const void* x;
   int64_t xsb, xsh, xss;
@@ -632,6 +667,7 @@ struct NormBwdParams {
   int64_t dsb, dsh, dss;
   const float* w;
   float* dw;
+  float* ws;  // per-block partial dw, gridDim.x x D
   int B, H, S;
   float eps;
   const float* cos_tab;
@@ -709,7 +745,26 @@ __global__ __launch_bounds__(256) void norm_rope_bwd_kernel(NormBwdParams p) {
   for (int d = threadIdx.x; d < D; d += 256) {
     float t = 0.f;
     for (int i = 0; i < RPB; ++i) t += dws[i][d];
-    atomicAdd(p.dw + d, t);
+    p.ws[(int64_t)blockIdx.x * D + d] = t;
+  }
+}
+
+// dw[d] = sum of the nblk partials in block order: 256 threads, thread t adds
+// blocks t / D, t / D + 256 / D, ... of column t % D, then the 256 / D column
+// sums are added in thread order.
+template <int D>
+__global__ __launch_bounds__(256) void norm_dw_reduce_kernel(const float* ws, int nblk, float* dw) {
+  constexpr int LANES = 256 / D;
+  __shared__ float part[LANES][D];
+  const int d = threadIdx.x % D, l = threadIdx.x / D;
+  float t = 0.f;
+  for (int i = l; i < nblk; i += LANES) t += ws[(int64_t)i * D + d];
+  part[l][d] = t;
+  __syncthreads();
+  if (l == 0) {
+    float s = 0.f;
+    for (int i = 0; i < LANES; ++i) s += part[i][d];
+    dw[d] = s;
   }
 }
 
@@ -722,14 +777,15 @@ extern "C" int64_t nq_attn_bwd_workspace_bytes(int B, int Hq, int S) {
   return (int64_t)B * Hq * ((S + 31) / 32) * 64 * (int64_t)sizeof(float);
 }
 
-extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                           const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
-                           const void* dout, const int64_t* do_strides, const float* lse,
-                           const int32_t* key_lens, void* dq,
-                           const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
-                           const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
-                           int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream) {
-  nq_clear_error();
+// Shared by nq_attn_bwd and nq_attn_bwd_bias (bias == NULL: none).
+static int bwd_entry(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                     const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
+                     const void* dout, const int64_t* do_strides, const float* lse, const int32_t* key_lens,
+                     const void* bias, const int64_t* bias_strides, const void* bias_t,
+                     const int64_t* bias_t_strides, void* dq, const int64_t* dq_strides, void* dk,
+                     const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
+                     int64_t workspace_bytes, int B, int Hq, int Hkv, int S, int T, int D, int dtype, int causal,
+                     float sm_scale, void* stream) {
   if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || T <= 0)
@@ -757,6 +813,16 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
     if (rs < 0 || rs * esz * BW_BN >= (int64_t(1) << 31))
       return nq_fail(NQ_ERR_UNSUPPORTED, "k/v sequence stride %lld too large", (long long)rs);
   if (!lse) return nq_fail(NQ_ERR_INVALID, "the forward's LSE is required");
+  if (bias) {
+    if (!bias_strides || !bias_t || !bias_t_strides)
+      return nq_fail(NQ_ERR_INVALID, "the bias needs its strides and its transpose");
+    for (const int64_t* bs : {bias_strides, bias_t_strides})
+      for (int a = 0; a < 3; ++a)
+        if (bs[a] < 0 || bs[a] % 8)
+          return nq_fail(NQ_ERR_INVALID, "bias strides must be non-negative multiples of 8 elements");
+    if (!nq_aligned16(bias) || !nq_aligned16(bias_t))
+      return nq_fail(NQ_ERR_INVALID, "the bias and its transpose must be 16-byte aligned");
+  }
   const int64_t need = nq_attn_bwd_workspace_bytes(B, Hq, S);
   if (!workspace || workspace_bytes < need)
     return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
@@ -776,11 +842,17 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   p.dvsb = dv_strides[0]; p.dvsh = dv_strides[1]; p.dvss = dv_strides[2];
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
   p.kv_lens = key_lens;
+  p.bias = bias;
+  p.bias_t = bias_t;
+  if (bias) {
+    p.bsb = bias_strides[0]; p.bsh = bias_strides[1]; p.bss = bias_strides[2];
+    p.btsb = bias_t_strides[0]; p.btsh = bias_t_strides[1]; p.btss = bias_t_strides[2];
+  }
   // dQ workgroups: 8 waves (256 query rows: each K/V tile load serves twice
   // the rows) when that still gives enough workgroups to fill the device
   const int64_t wide_wgs = (int64_t)B * Hkv * ((S + 256 / G - 1) / (256 / G));
   const bool f32 = dtype == NQ_DTYPE_F32;  // fp32 tensors: the fp32 MFMA kernels (4 waves)
-  const int nw = (!f32 && wide_wgs >= BW_DQ_WIDE_MIN_WGS) ? 8 : 4;
+  const int nw = (!f32 && !bias && wide_wgs >= BW_DQ_WIDE_MIN_WGS) ? 8 : 4;
   p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
   p.coff = T - S;
@@ -793,9 +865,52 @@ extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* 
   return nq_check_launch(e);
 }
 
+extern "C" int nq_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
+                           const void* dout, const int64_t* do_strides, const float* lse,
+                           const int32_t* key_lens, void* dq,
+                           const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                           const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B, int Hq,
+                           int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale, void* stream) {
+  nq_clear_error();
+  return bwd_entry(q, q_strides, k, k_strides, v, v_strides, o, o_strides, dout, do_strides, lse, key_lens, nullptr,
+                   nullptr, nullptr, nullptr, dq, dq_strides, dk, dk_strides, dv, dv_strides, workspace,
+                   workspace_bytes, B, Hq, Hkv, S, T, D, dtype, causal, sm_scale, stream);
+}
+
+extern "C" int nq_attn_bwd_bias(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
+                                const void* dout, const int64_t* do_strides, const float* lse,
+                                const int32_t* key_lens, const void* bias, const int64_t* bias_strides,
+                                const void* bias_t, const int64_t* bias_t_strides, void* dq,
+                                const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                                const int64_t* dv_strides, void* workspace, int64_t workspace_bytes, int B,
+                                int Hq, int Hkv, int S, int T, int D, int dtype, int causal, float sm_scale,
+                                void* stream) {
+  nq_clear_error();
+  if (!bias) return nq_fail(NQ_ERR_INVALID, "nq_attn_bwd_bias needs the bias");
+  return bwd_entry(q, q_strides, k, k_strides, v, v_strides, o, o_strides, dout, do_strides, lse, key_lens, bias,
+                   bias_strides, bias_t, bias_t_strides, dq, dq_strides, dk, dk_strides, dv, dv_strides, workspace,
+                   workspace_bytes, B, Hq, Hkv, S, T, D, dtype, causal, sm_scale, stream);
+}
+
+// Blocks of the QK-Norm + RoPE backward (one per 256 / (D/16) rows, at most 1024).
+static int64_t norm_bwd_blocks(int B, int S, int H, int D) {
+  const int64_t rows = (int64_t)B * H * S;
+  const int rpb = 256 / (D / 16);
+  const int64_t blocks = (rows + rpb - 1) / rpb;
+  return blocks < 1024 ? blocks : 1024;
+}
+
+extern "C" int64_t nq_qk_norm_rope_bwd_workspace_bytes(int B, int S, int H, int D) {
+  if (B <= 0 || S <= 0 || H <= 0 || !head_dim_ok(D)) return 0;
+  return norm_bwd_blocks(B, S, H, D) * D * (int64_t)sizeof(float);
+}
+
 extern "C" int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, const void* dy,
                                    const int64_t* dy_strides, void* dx, const int64_t* dx_strides,
-                                   const float* weight, float* dweight, int B, int S, int H, int D, int dtype,
+                                   const float* weight, float* dweight, void* workspace, int64_t workspace_bytes,
+                                   int B, int S, int H, int D, int dtype,
                                    float eps, const float* cos_tab, const float* sin_tab, int max_pos,
                                    const int32_t* pos, const int32_t* pos_base, int pos0, void* stream) {
   nq_clear_error();
@@ -806,6 +921,12 @@ extern "C" int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, cons
     return nq_fail(NQ_ERR_INVALID, "x, dy, dx and their strides are required");
   if ((weight == nullptr) != (dweight == nullptr))
     return nq_fail(NQ_ERR_INVALID, "weight and dweight go together");
+  if (weight) {
+    const int64_t need = nq_qk_norm_rope_bwd_workspace_bytes(B, S, H, D);
+    if (!workspace || workspace_bytes < need)
+      return nq_fail(NQ_ERR_WORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
+                     (long long)workspace_bytes);
+  }
   if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
   if (!nq_aligned16(x) || !nq_aligned16(dy) || !nq_aligned16(dx))
@@ -818,19 +939,18 @@ extern "C" int nq_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, cons
   p.x = x; p.xsb = x_strides[0]; p.xsh = x_strides[1]; p.xss = x_strides[2];
   p.dy = dy; p.ysb = dy_strides[0]; p.ysh = dy_strides[1]; p.yss = dy_strides[2];
   p.dx = dx; p.dsb = dx_strides[0]; p.dsh = dx_strides[1]; p.dss = dx_strides[2];
-  p.w = weight; p.dw = dweight;
+  p.w = weight; p.dw = dweight; p.ws = reinterpret_cast<float*>(workspace);
   p.B = B; p.H = H; p.S = S; p.eps = eps;
   p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.max_pos = max_pos;
   p.pos = pos; p.pos_base = pos_base; p.pos0 = pos0;
-  const int64_t rows = (int64_t)B * H * S;
-  const int rpb = 256 / (D / 16);
-  const int64_t blocks = (rows + rpb - 1) / rpb;
-  const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024));
+  const int nblk = (int)norm_bwd_blocks(B, S, H, D);
+  const dim3 grid((unsigned)nblk);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   with_head_dim(D, [&](auto dc) {
     constexpr int DD = decltype(dc)::value;
     if (dtype == NQ_DTYPE_BF16) hipLaunchKernelGGL((norm_rope_bwd_kernel<bf16, DD>), grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL((norm_rope_bwd_kernel<float, DD>), grid, dim3(256), 0, st, p);
+    if (weight) hipLaunchKernelGGL((norm_dw_reduce_kernel<DD>), dim3(1), dim3(256), 0, st, p.ws, nblk, dweight);
     return 0;
   });
   return nq_check_launch(hipGetLastError());

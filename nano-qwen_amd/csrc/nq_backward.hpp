@@ -29,6 +29,14 @@ struct BwdParams {
   // key padding: sequence b attends keys [0, kv_lens[b]) (clamped to
   // [0, T]; the rest get zero gradients); NULL = all T keys
   const int32_t* kv_lens;
+  // additive attention bias as in the forward (bias[b, h, i, j], keys
+  // contiguous, rows readable up to T rounded up to 8), and its transpose
+  // bias_t[b, h, j, i] (queries contiguous, rows readable up to S rounded up
+  // to 8) for the dK/dV kernel, whose lanes hold keys; NULL = no bias
+  const void* bias;
+  int64_t bsb, bsh, bss;
+  const void* bias_t;
+  int64_t btsb, btsh, btss;
 };
 
 // Keys sequence b attends.

@@ -73,7 +73,9 @@ struct TileCopy {
 };
 
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL>
+// BIAS: the forward's additive bias (p.bias) enters every score; a row the
+// bias masks entirely has LSE -inf and P = 0 (its scratch LSE is stored +inf).
+template <int D, bool CAUSAL, bool BIAS = false>
 __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
   using L = BwF32<D>;
   constexpr int NT = D / 2, NDO = D / 32;
@@ -126,12 +128,16 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
     }
     dlt = xor32_sum(acc);
   }
-  const float lse2 = p.lse[((int64_t)b * p.Hq + head) * p.S + qi_c] * kLog2e;
+  float lse2 = p.lse[((int64_t)b * p.Hq + head) * p.S + qi_c] * kLog2e;
+  if (BIAS && !(lse2 > -INFINITY)) lse2 = INFINITY;  // no key kept: P = exp2(s - inf) = 0
   if (qvalid && hh == 0) {
     const int64_t wi = bw_ws_index(p, b, head, qi);
     p.ws[wi] = lse2;
     p.ws[wi + 32] = dlt;
   }
+  const float* brow = BIAS ? reinterpret_cast<const float*>(p.bias) + b * p.bsb + head * p.bsh +
+                                 (int64_t)qi_c * p.bss
+                           : nullptr;
   if (qblk == p.nqb - 1) {  // scratch slots past S: zero
     const int pad = p.nst * 32 - p.S;
     for (int t = threadIdx.x; t < p.G * 32; t += 64 * BF32_NW) {
@@ -169,11 +175,22 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
     }
     const int n0 = j * BF32_TILE;
     const int lim = CAUSAL ? min(Tk - 1, qi + p.coff) : Tk - 1;
+    float bsv[16];
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k4 = n0 + r * 8 + hh * 4;
+        const floatx4 bv = k4 < Tk ? *reinterpret_cast<const floatx4*>(brow + k4) : floatx4{};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bsv[r * 4 + e] = bv[e] * kLog2e;
+      }
+    }
     float ds[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int key = n0 + (i / 4) * 8 + hh * 4 + (i % 4);
-      const float pe = key <= lim ? fast_exp2(s[i] * p.scale_log2 - lse2) : 0.f;
+      const float x = BIAS ? __builtin_fmaf(s[i], p.scale_log2, bsv[i]) - lse2 : s[i] * p.scale_log2 - lse2;
+      const float pe = key <= lim ? fast_exp2(x) : 0.f;
       ds[i] = pe * (dp[i] - dlt);
     }
     // dQ^T += K^T dS^T: step t, k-slot hh = key (t/4)*8 + hh*4 + t%4
@@ -198,7 +215,7 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dq_f32_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool BIAS = false>
 __global__ void __launch_bounds__(64 * BF32_NW) bwd_dkdv_f32_kernel(BwdParams p) {
   using L = BwF32<D>;
   constexpr int NT = D / 2, NDO = D / 32;
@@ -272,12 +289,26 @@ __global__ void __launch_bounds__(64 * BF32_NW) bwd_dkdv_f32_kernel(BwdParams p)
           dp = mfma_f32x2(c[e], vr[4 * t4 + e], dp);
         }
       }
+      float bsv[16];
+      if constexpr (BIAS) {
+        // the transposed bias: this key's row, the tile's queries in runs of 4
+        const float* brow = reinterpret_cast<const float*>(p.bias_t) + b * p.btsb + head * p.btsh +
+                            (int64_t)(kattend ? key : 0) * p.btss;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int q4 = s0 + r * 8 + hh * 4;
+          const floatx4 bv = (kattend && q4 < p.S) ? *reinterpret_cast<const floatx4*>(brow + q4) : floatx4{};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bsv[r * 4 + e] = bv[e] * kLog2e;
+        }
+      }
       float pe[16], ds[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ql = (i / 4) * 8 + hh * 4 + (i % 4);
         const bool keep = kattend && (!CAUSAL || key <= s0 + ql + p.coff);
-        pe[i] = keep ? fast_exp2(s[i] * p.scale_log2 - lse2s[ql]) : 0.f;
+        const float x = BIAS ? __builtin_fmaf(s[i], p.scale_log2, bsv[i]) - lse2s[ql] : s[i] * p.scale_log2 - lse2s[ql];
+        pe[i] = keep ? fast_exp2(x) : 0.f;
         ds[i] = pe[i] * (dp[i] - dlts[ql]);
       }
       // dV^T += dO^T P and dK^T += Q^T dS: step t, k-slot hh = query row
@@ -314,6 +345,16 @@ static hipError_t launch_f32(const BwdParams& p, bool causal, hipStream_t st) {
   const dim3 block(64 * BF32_NW);
   const dim3 gq((unsigned)(p.nqb * p.B * p.Hkv));
   const dim3 gk((unsigned)(((p.T + 32 * BF32_NW - 1) / (32 * BF32_NW)) * p.B * p.Hkv));
+  if (p.bias) {
+    if (causal) {
+      hipLaunchKernelGGL((bwd_dq_f32_kernel<D, true, true>), gq, block, 0, st, p);
+      hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, true, true>), gk, block, 0, st, p);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_f32_kernel<D, false, true>), gq, block, 0, st, p);
+      hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, false, true>), gk, block, 0, st, p);
+    }
+    return hipGetLastError();
+  }
   if (causal) {
     hipLaunchKernelGGL((bwd_dq_f32_kernel<D, true>), gq, block, 0, st, p);
     hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, true>), gk, block, 0, st, p);

@@ -117,7 +117,11 @@ struct PfTile {
 // sequence b is row t % page of page bt[b * bts + t / page], pool strides
 // (ksb, ksh, kss) = (page, head, row)); page % 32 == 0, so each 32-row half of
 // a 64-key tile lies in one page.
-template <int D, typename T, bool CAUSAL, bool FUSE_Q, int NW, bool PAGED = false>
+// BIAS: an additive bias per (query, key) (p.bias, SDPA's attn_mask) is added
+// to every score tile before the row max, so every step takes the masked
+// path; a row may then see no finite score in its first tiles (or in none),
+// which the running max starts from a placeholder for (below).
+template <int D, typename T, bool CAUSAL, bool FUSE_Q, int NW, bool PAGED = false, bool BIAS = false>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW),
                                amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(PrefillParams p) {
@@ -466,10 +470,29 @@ prefill_kernel(PrefillParams p) {
   // for R < 2^16, without the integer-division sequence and its constants
   const float inv_g = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, 1.0f / (float)p.G)));
   auto mask_tile = [&](floatx16* s, int n0) {
-    if ((n0 + PF_BN > Tk) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff)) {
+    if (BIAS || (n0 + PF_BN > Tk) || (CAUSAL && n0 + PF_BN - 1 > q0 + coff)) {
       const int ml = fresh_lane();
       const int mhh = ml >> 5;
-      const int mqi = q0 + (int)(((float)(wave * 32 + (ml & 31)) + 0.5f) * inv_g);
+      const int mR = wave * 32 + (ml & 31);
+      const int mqi = q0 + (int)(((float)mR + 0.5f) * inv_g);
+      if constexpr (BIAS) {
+        // the lane's 32 scores are 4 runs of 8 consecutive keys: one 16-byte
+        // read each (runs starting past the keys are masked below anyway)
+        const int mg = mR - (mqi - q0) * p.G;
+        const bf16* brow = reinterpret_cast<const bf16*>(p.bias) + b * p.bsb + (kvh * p.G + mg) * p.bsh +
+                           (int64_t)min(mqi, p.S - 1) * p.bss;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int k8 = n0 + kb * 32 + h2 * 16 + mhh * 8;
+            if (k8 < Tk) {
+              const bf16x8 bv = *reinterpret_cast<const bf16x8*>(brow + k8);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) s[kb][h2 * 8 + e] += (float)bv[e] * kLog2e;
+            }
+          }
+      }
       const int lim = CAUSAL ? min(Tk - 1, mqi + coff) : Tk - 1;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -486,6 +509,9 @@ prefill_kernel(PrefillParams p) {
   // here; later tiles carry the offset from their MFMAs.)  mx_cur is the row
   // max of the next tile to be exponentiated, relative to m_i.
   float mx_cur = 0.f;
+  // BIAS: a row with no finite score yet holds the placeholder max 0 (ph);
+  // its first finite tile max then replaces it outright (O and l are still 0)
+  bool ph = false;
   {
     mask_tile(sA, 0);
     float mx = -INFINITY;
@@ -493,7 +519,14 @@ prefill_kernel(PrefillParams p) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(sA[kb][i], sA[kb][i + 1]));
-    set_max(xor32_max(mx));
+    mx = xor32_max(mx);
+    if constexpr (BIAS) {
+      ph = !(mx > -INFINITY);
+      if (ph) mx = 0.f;
+      // S[0] relative to the placeholder is all -inf: no max to take from it
+      if (ph) mx_cur = -INFINITY;
+    }
+    set_max(mx);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) sA[kb] -= m_i;
   }
@@ -523,11 +556,21 @@ prefill_kernel(PrefillParams p) {
 
     // online softmax (log2 domain); each lane owns one query row
     (void)n0;
-    if (wave_any(mx_cur > PF_RESCALE_LOG2)) {
+    bool raise = mx_cur > PF_RESCALE_LOG2;
+    if constexpr (BIAS) raise = raise || (ph && mx_cur > -INFINITY);
+    if (wave_any(raise)) {
       const float m_old = m_i;
-      set_max(m_i + fmaxf(mx_cur, 0.f));
+      float inc = fmaxf(mx_cur, 0.f);
+      if constexpr (BIAS) {
+        if (ph) inc = mx_cur > -INFINITY ? mx_cur : 0.f;
+      }
+      set_max(m_i + inc);
       const float delta = m_i - m_old;
-      const float alpha = fast_exp2(-delta);
+      float alpha = fast_exp2(-delta);
+      if constexpr (BIAS) {
+        if (ph) alpha = 0.f;  // nothing accumulated yet (avoids 0 * inf)
+        ph = ph && !(mx_cur > -INFINITY);
+      }
       l_i *= alpha;
 #pragma unroll
       for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
@@ -628,7 +671,7 @@ prefill_kernel(PrefillParams p) {
   // step whose next tile is one of them carries no mask branch.  That branch would
   // split the step into basic blocks, and the compiler would then sink the exp2
   // work of P[j] below the S[j+1] MFMAs it is meant to interleave with.
-  const int jfree = min(ntiles, min(Tk / PF_BN, CAUSAL ? (q0 + coff + 1) / PF_BN : ntiles));
+  const int jfree = BIAS ? 0 : min(ntiles, min(Tk / PF_BN, CAUSAL ? (q0 + coff + 1) / PF_BN : ntiles));
   int j = 0;
   for (; j + 2 < jfree; j += 2) {
     step(I0{}, Yes{}, No{}, j);
@@ -646,7 +689,8 @@ prefill_kernel(PrefillParams p) {
   }
 
   l_i = xor32_sum(l_i);
-  const float inv_l = 1.f / l_i;
+  // (BIAS: a row the bias masks entirely has l = 0 and gets zeros, as SDPA gives)
+  const float inv_l = (BIAS && !(l_i > 0.f)) ? 0.f : 1.f / l_i;
 
   // ---- epilogue: O goes through LDS, so that every store instruction writes
   // whole rows (16 lanes x 16 contiguous bytes per row) instead of 8-byte
@@ -684,7 +728,9 @@ prefill_kernel(PrefillParams p) {
   if (p.lse && ehh == 0) {
     const int eR = wave * 32 + er32;
     const int eq = q0 + eR / p.G;
-    if (eq < p.S) p.lse[((int64_t)b * p.Hq + kvh * p.G + eR % p.G) * p.S + eq] = (m_i + __log2f(l_i)) * kLn2;
+    if (eq < p.S)
+      p.lse[((int64_t)b * p.Hq + kvh * p.G + eR % p.G) * p.S + eq] =
+          (BIAS && !(l_i > 0.f)) ? -INFINITY : (m_i + __log2f(l_i)) * kLn2;
   }
 }
 
@@ -692,6 +738,14 @@ template <int D, typename T, int NW>
 static hipError_t launch_prefill_nw(const PrefillParams& p, bool causal, bool fuse, hipStream_t st) {
   dim3 grid((unsigned)(p.nqb * p.B * p.Hkv));
   dim3 block(64 * NW);
+  if (p.bias) {  // an attention bias: 4-wave workgroups, the fused-Q instance, dense K/V
+    if constexpr (NW == 4) {
+      if (causal) hipLaunchKernelGGL((prefill_kernel<D, T, true, true, 4, false, true>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((prefill_kernel<D, T, false, true, 4, false, true>), grid, block, 0, st, p);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
   if (p.bt) {  // paged pools: the fused-Q instance (its norm and rotation are skipped when not given)
     if (causal) hipLaunchKernelGGL((prefill_kernel<D, T, true, true, NW, true>), grid, block, 0, st, p);
     else hipLaunchKernelGGL((prefill_kernel<D, T, false, true, NW, true>), grid, block, 0, st, p);
@@ -721,9 +775,11 @@ static hipError_t launch_prefill(const PrefillParams& p, int nw, bool causal, bo
 
 using namespace nq;
 
-// Shared by the dense and paged entry points: bt == NULL for dense K/V.
+// Shared by the dense, paged and bias entry points: bt == NULL for dense K/V,
+// bias == NULL for none.
 static int prefill_entry(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                          const void* v, const int64_t* v_strides, const int32_t* bt, int64_t bts, int page,
+                         const void* bias, const int64_t* bias_strides,
                          void* o, const int64_t* o_strides, float* lse, const int32_t* key_lens, int B, int Hq,
                          int Hkv, int S, int T, int D, int dtype, const float* q_weight, float eps,
                          const float* cos_tab, const float* sin_tab, int max_pos, const int32_t* q_pos,
@@ -755,6 +811,16 @@ static int prefill_entry(const void* q, const int64_t* q_strides, const void* k,
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
   if (!nq_aligned16(cos_tab) || !nq_aligned16(sin_tab))  // their rows are DMA'd to LDS in 16-byte pieces
     return nq_fail(NQ_ERR_INVALID, "cos/sin tables must be 16-byte aligned");
+  if (bias) {
+    if (bt) return nq_fail(NQ_ERR_UNSUPPORTED, "an attention bias is taken with dense K/V only");
+    if (!bias_strides) return nq_fail(NQ_ERR_INVALID, "the bias needs its strides");
+    if (!f32 && 128 % G) return nq_fail(NQ_ERR_UNSUPPORTED, "with a bias the GQA group size %d must divide 128", G);
+    // 8 consecutive keys per vector read
+    if (!nq_aligned16(bias) || bias_strides[0] % 8 || bias_strides[1] % 8 || bias_strides[2] % 8 ||
+        bias_strides[0] < 0 || bias_strides[1] < 0 || bias_strides[2] < 0)
+      return nq_fail(NQ_ERR_INVALID, "the bias must be 16-byte aligned with non-negative strides that are multiples "
+                     "of 8 elements");
+  }
   PrefillParams p{};
   p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse;
   p.qsb = q_strides[0]; p.qsh = q_strides[1]; p.qss = q_strides[2];
@@ -766,6 +832,8 @@ static int prefill_entry(const void* q, const int64_t* q_strides, const void* k,
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.S = S; p.T = T;
   p.kv_lens = key_lens; p.kv_extra = 0; p.kv_max = T;
   p.bt = bt; p.bts = bts; p.page = page;
+  p.bias = bias;
+  if (bias) { p.bsb = bias_strides[0]; p.bsh = bias_strides[1]; p.bss = bias_strides[2]; }
   const float scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
   const bool fuse = q_weight != nullptr || cos_tab != nullptr;
@@ -779,7 +847,7 @@ static int prefill_entry(const void* q, const int64_t* q_strides, const void* k,
   const int64_t wide_wgs = (int64_t)B * Hkv * ((S + PF_MAX_ROWS / G - 1) / (PF_MAX_ROWS / G));
   // (a D = 32 tile is 4 KiB: one 1 KiB load per wave of a 4-wave workgroup,
   // too few for eight waves)
-  const int nw = (128 % G == 0 && (wide_wgs < PF_WIDE_MIN_WGS || D == 32)) ? 4 : 8;
+  const int nw = (128 % G == 0 && (wide_wgs < PF_WIDE_MIN_WGS || D == 32 || bias)) ? 4 : 8;
   p.BM = 32 * nw / G;
   p.nqb = (S + p.BM - 1) / p.BM;
   const hipError_t e =
@@ -797,9 +865,24 @@ extern "C" int nq_attn_prefill_fwd(const void* q, const int64_t* q_strides, cons
                                    const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0,
                                    int causal, float sm_scale, void* stream) {
   nq_clear_error();
-  return prefill_entry(q, q_strides, k, k_strides, v, v_strides, nullptr, 0, 0, o, o_strides, lse, key_lens, B,
-                       Hq, Hkv, S, T, D, dtype, q_weight, eps, cos_tab, sin_tab, max_pos, q_pos, q_pos_base,
-                       q_pos0, causal, sm_scale, stream);
+  return prefill_entry(q, q_strides, k, k_strides, v, v_strides, nullptr, 0, 0, nullptr, nullptr, o, o_strides, lse,
+                       key_lens, B, Hq, Hkv, S, T, D, dtype, q_weight, eps, cos_tab, sin_tab, max_pos, q_pos,
+                       q_pos_base, q_pos0, causal, sm_scale, stream);
+}
+
+extern "C" int nq_attn_prefill_bias_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                        const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                        void* o, const int64_t* o_strides, float* lse, const int32_t* key_lens,
+                                        const void* bias, const int64_t* bias_strides, int B, int Hq, int Hkv,
+                                        int S, int T, int D, int dtype, const float* q_weight, float eps,
+                                        const float* cos_tab, const float* sin_tab, int max_pos,
+                                        const int32_t* q_pos, const int32_t* q_pos_base, int q_pos0, int causal,
+                                        float sm_scale, void* stream) {
+  nq_clear_error();
+  if (!bias) return nq_fail(NQ_ERR_INVALID, "nq_attn_prefill_bias_fwd needs the bias");
+  return prefill_entry(q, q_strides, k, k_strides, v, v_strides, nullptr, 0, 0, bias, bias_strides, o, o_strides,
+                       lse, key_lens, B, Hq, Hkv, S, T, D, dtype, q_weight, eps, cos_tab, sin_tab, max_pos, q_pos,
+                       q_pos_base, q_pos0, causal, sm_scale, stream);
 }
 
 extern "C" int nq_attn_prefill_paged_fwd(const void* q, const int64_t* q_strides, const void* k_pool,
@@ -819,6 +902,6 @@ extern "C" int nq_attn_prefill_paged_fwd(const void* q, const int64_t* q_strides
     return nq_fail(NQ_ERR_INVALID, "bt_stride %lld holds fewer than the %d pages of T %d", (long long)bt_stride,
                    (T + page_size - 1) / page_size, T);
   return prefill_entry(q, q_strides, k_pool, k_pool_strides, v_pool, v_pool_strides, block_table, bt_stride,
-                       page_size, o, o_strides, lse, nullptr, B, Hq, Hkv, S, T, D, dtype, q_weight, eps, cos_tab,
-                       sin_tab, max_pos, q_pos, q_pos_base, q_pos0, causal, sm_scale, stream);
+                       page_size, nullptr, nullptr, o, o_strides, lse, nullptr, B, Hq, Hkv, S, T, D, dtype, q_weight,
+                       eps, cos_tab, sin_tab, max_pos, q_pos, q_pos_base, q_pos0, causal, sm_scale, stream);
 }

@@ -34,11 +34,17 @@ struct PrefillParams {
   // keys - 1.
   const int32_t* kv_lens;
   int kv_extra, kv_max;
-  // paged K/V (fp32 kernel): key t of sequence b is row t % page of page
+  // paged K/V (NULL bt = dense): key t of sequence b is row t % page of page
   // bt[b * bts + t / page], strides (ksb, ksh, kss) = (page, head, row)
   const int32_t* bt;
   int64_t bts;
   int page;
+  // additive attention bias (SDPA's attn_mask: a bool mask as 0 / -inf, or a
+  // float mask), in the kernel's element type: bias[b, h, i, j] at
+  // b * bsb + h * bsh + i * bss + j (0 strides broadcast), each row's keys
+  // contiguous and readable up to T rounded up to a multiple of 8
+  const void* bias;
+  int64_t bsb, bsh, bss;
 };
 
 // Keys of sequence b (-1: a length out of range).

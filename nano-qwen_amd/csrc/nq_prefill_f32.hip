@@ -41,7 +41,9 @@ struct F32Tile {
   __device__ static int vswz(int r) { return CPR >= 16 ? (((r >> 2) & 1) << 3) : 0; }
 };
 
-template <int D, bool CAUSAL, bool FUSE_Q>
+// BIAS: p.bias (fp32) is added to every score; a row may then see no finite
+// score in a tile, or in any (zeros out, LSE -inf, as SDPA gives).
+template <int D, bool CAUSAL, bool FUSE_Q, bool BIAS = false>
 __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams p) {
   using Tl = F32Tile<D>;
   constexpr int CPR = Tl::CPR;
@@ -177,9 +179,20 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
       for (int e = 0; e < 4; ++e) s = mfma32_f32(a[e], x[4 * t4 + e], s);
     }
 
-    // keys past T, and (causal) keys past this row's frontier
     const int n0 = j * PF32_BN;
-    if (n0 + PF32_BN > T || (CAUSAL && n0 + PF32_BN - 1 > q0 + coff)) {
+    if constexpr (BIAS) {
+      // scores to log2 units plus the bias (the lane's keys: 4 runs of 4)
+      const float* brow = reinterpret_cast<const float*>(p.bias) + b * p.bsb + head * p.bsh + (int64_t)qi_c * p.bss;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k4 = n0 + r * 8 + hh * 4;
+        const floatx4 bv = k4 < T ? *reinterpret_cast<const floatx4*>(brow + k4) : floatx4{};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[r * 4 + e] = __builtin_fmaf(bv[e], kLog2e, s[r * 4 + e] * p.scale_log2);
+      }
+    }
+    // keys past T, and (causal) keys past this row's frontier
+    if (BIAS || n0 + PF32_BN > T || (CAUSAL && n0 + PF32_BN - 1 > q0 + coff)) {
       const int lim = CAUSAL ? min(T - 1, qi + coff) : T - 1;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -187,12 +200,14 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
     }
 
     // online softmax in the log2 domain (tile 0 holds key 0 for every row,
-    // so m_i is finite from the first tile on)
+    // so m_i is finite from the first tile on, unless a bias masks it: a row
+    // with no finite score yet keeps m_i = -inf and exponentiates against 0)
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
-    const float m_new = fmaxf(m_i, xor32_max(mx) * p.scale_log2);
-    const float alpha = fast_exp2(m_i - m_new);
+    const float m_new = fmaxf(m_i, xor32_max(mx) * (BIAS ? 1.f : p.scale_log2));
+    const float m_use = (BIAS && !(m_new > -INFINITY)) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_i - m_use);
     l_i *= alpha;
 #pragma unroll
     for (int dd = 0; dd < NDO; ++dd) oacc[dd] *= alpha;
@@ -201,7 +216,7 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
     float ls = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      pv[i] = fast_exp2(s[i] * p.scale_log2 - m_i);
+      pv[i] = BIAS ? fast_exp2(s[i] - m_use) : fast_exp2(s[i] * p.scale_log2 - m_i);
       ls += pv[i];
     }
     l_i += ls;
@@ -232,7 +247,8 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
     if (p.lse && hh == 0) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = -INFINITY;
     return;
   }
-  const float inv_l = 1.f / l_i;
+  const bool none = BIAS && !(l_i > 0.f);  // every key masked by the bias: zeros, as SDPA gives
+  const float inv_l = none ? 0.f : 1.f / l_i;
 #pragma unroll
   for (int dd = 0; dd < NDO; ++dd)
 #pragma unroll
@@ -241,13 +257,19 @@ __global__ void __launch_bounds__(64 * PF32_NW) prefill_f32_kernel(PrefillParams
                          oacc[dd][gq * 4 + 2] * inv_l, oacc[dd][gq * 4 + 3] * inv_l};
       *reinterpret_cast<floatx4*>(orow + dd * 32 + gq * 8 + hh * 4) = t;
     }
-  if (p.lse && hh == 0) p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = (m_i + __log2f(l_i)) * kLn2;
+  if (p.lse && hh == 0)
+    p.lse[((int64_t)b * p.Hq + head) * p.S + qi] = none ? -INFINITY : (m_i + __log2f(l_i)) * kLn2;
 }
 
 template <int D>
 static hipError_t launch_f32(const PrefillParams& p, bool causal, bool fuse, hipStream_t st) {
   dim3 grid((unsigned)(p.nqb * p.B * p.Hkv));
   dim3 block(64 * PF32_NW);
+  if (p.bias) {
+    if (causal) hipLaunchKernelGGL((prefill_f32_kernel<D, true, true, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((prefill_f32_kernel<D, false, true, true>), grid, block, 0, st, p);
+    return hipGetLastError();
+  }
   if (causal) {
     if (fuse) hipLaunchKernelGGL((prefill_f32_kernel<D, true, true>), grid, block, 0, st, p);
     else hipLaunchKernelGGL((prefill_f32_kernel<D, true, false>), grid, block, 0, st, p);

@@ -11,6 +11,9 @@ forward signature and the returned dict are the reference's
 Only attention runs on the gfx950 kernels; embedding, the layer RMSNorms,
 SwiGLU and the LM head are the reference's torch ops (hipBLASLt GEMMs).  MoE
 layers (model/moe.py) are outside the attention hot path and not provided.
+``gradient_checkpointing`` (config field and attribute, transformer.py:92,
+121-127) recomputes each block in the backward when training, as the
+reference does.
 """
 
 from __future__ import annotations
@@ -21,6 +24,7 @@ from typing import List, Optional
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+import torch.utils.checkpoint as checkpoint_utils
 
 from .attention import Attention, KVCache
 from .config import AttentionConfig
@@ -35,6 +39,7 @@ class ModelConfig(AttentionConfig):
     intermediate_size: int = 11008
     tie_word_embeddings: bool = False
     initializer_range: float = 0.02
+    gradient_checkpointing: bool = False
 
 
 class LayerRMSNorm(nn.Module):
@@ -120,6 +125,8 @@ class Qwen3Model(nn.Module):
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
         if getattr(config, "tie_word_embeddings", False):
             self.lm_head.weight = self.embed.embed_tokens.weight
+        # transformer.py:92: each block recomputed in the backward when training
+        self.gradient_checkpointing = getattr(config, "gradient_checkpointing", False)
         self.apply(self._init_weights)
 
     def _init_weights(self, module: nn.Module) -> None:
@@ -147,7 +154,14 @@ class Qwen3Model(nn.Module):
         hidden_states = self.embed(input_ids)
         for i, layer in enumerate(self.layers):
             kv_cache = kv_caches[i] if kv_caches is not None else None
-            hidden_states, _ = layer(hidden_states, position_ids, attention_mask, kv_cache)
+            if self.gradient_checkpointing and self.training:
+                # transformer.py:121-127: the block's activations (the attention
+                # kernels' Q-hat, K-hat, O and LSE included) are dropped and the
+                # block's forward runs again inside the backward
+                hidden_states, _ = checkpoint_utils.checkpoint(
+                    layer, hidden_states, position_ids, attention_mask, kv_cache, use_reentrant=False)
+            else:
+                hidden_states, _ = layer(hidden_states, position_ids, attention_mask, kv_cache)
         hidden_states = self.norm(hidden_states)
         logits = self.lm_head(hidden_states)
         loss = None

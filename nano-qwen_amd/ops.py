@@ -24,6 +24,7 @@ from . import _lib
 __all__ = [
     "KernelCall",
     "qk_norm_rope",
+    "AttnBias",
     "attention_prefill",
     "attention_prefill_paged",
     "attention_decode",
@@ -269,6 +270,53 @@ def qk_norm_rope(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = N
 # Prefill
 # ---------------------------------------------------------------------------
 
+class AttnBias:
+    """SDPA's ``attn_mask`` in the form the kernels read: an additive bias.
+
+    model/attention.py:110-113 hands ``attention_mask`` to SDPA, which takes a
+    bool keep-mask (True = attend) or a float mask added to the scores, either
+    broadcastable to (B, Hq, S, T).  Here a bool mask becomes 0 / -inf and a
+    float mask keeps its values, in the kernels' element type.  ``bias`` keeps
+    the mask's broadcast batch / head / query axes (stride 0) and materialises
+    the key axis, padded to a multiple of 8 keys (the kernels read 8 keys at a
+    time); ``bias_t`` (built when ``transpose``) holds the transpose
+    (B|1, Hq|1, T, S padded to 8) for the backward's dK/dV kernel, whose lanes
+    hold keys.  A row whose keys are all masked gives zeros (and LSE -inf), as
+    SDPA does.
+    """
+
+    def __init__(self, mask: torch.Tensor, B: int, Hq: int, S: int, T: int, dtype: torch.dtype, device,
+                 transpose: bool = False):
+        if mask.dim() > 4 or mask.dim() == 0:
+            raise ValueError(f"attn_mask must have 1 to 4 dims, got shape {tuple(mask.shape)}")
+        m = mask.reshape((1,) * (4 - mask.dim()) + tuple(mask.shape))  # SDPA's broadcast alignment
+        for got, want, name in zip(m.shape, (B, Hq, S, T), ("batch", "heads", "queries", "keys")):
+            if got not in (1, want):
+                raise ValueError(f"attn_mask of shape {tuple(mask.shape)} does not broadcast to "
+                                 f"(B, Hq, S, T) = {(B, Hq, S, T)} on the {name} axis")
+        m = m.to(device)
+        if m.dtype == torch.bool:
+            add = torch.zeros(m.shape, dtype=dtype, device=device).masked_fill_(~m, float("-inf"))
+        elif m.is_floating_point():
+            add = m.to(dtype)
+        else:
+            raise TypeError(f"attn_mask must be bool or floating point, got {m.dtype}")
+        Bm, Hm, Sm = add.shape[:3]
+        self.shape = (B, Hq, S, T)
+        self.bias = torch.zeros(Bm, Hm, Sm, -(-T // 8) * 8, dtype=dtype, device=device)
+        self.bias[..., :T] = add
+        self.strides = self._strides(self.bias, (Bm, Hm, Sm))
+        self.bias_t, self.t_strides = None, None
+        if transpose:
+            self.bias_t = torch.zeros(Bm, Hm, T, -(-S // 8) * 8, dtype=dtype, device=device)
+            self.bias_t[..., :S] = add.expand(Bm, Hm, S, T).transpose(-1, -2)
+            self.t_strides = self._strides(self.bias_t, (Bm, Hm, T))
+
+    @staticmethod
+    def _strides(t: torch.Tensor, sizes):
+        return tuple(t.stride(i) if sizes[i] > 1 else 0 for i in range(3))
+
+
 def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                       q_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
                       cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
@@ -276,6 +324,7 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                       pos_base: Optional[torch.Tensor] = None,
                       causal: bool = True, sm_scale: Optional[float] = None,
                       key_lens: Optional[torch.Tensor] = None,
+                      bias: Optional[AttnBias] = None,
                       out: Optional[torch.Tensor] = None, return_lse: bool = False,
                       plan: bool = False):
     """GQA prefill attention with QK-Norm + RoPE of Q fused into its load.
@@ -284,7 +333,8 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     are None); k: (B, Hkv, T, D) keys as stored (already normed and rotated);
     v: (B, Hkv, T, D).  ``causal`` keeps key j for query i iff j <= i + T - S.
     ``key_lens`` (int, (B,)) limits sequence b to keys [0, key_lens[b]): key
-    padding.  Returns o shaped (B, Hq, S, D); by default it is a transposed view of a
+    padding.  ``bias`` (an ``AttnBias``) adds SDPA's general attn_mask to the
+    scores.  Returns o shaped (B, Hq, S, D); by default it is a transposed view of a
     contiguous (B, S, Hq, D) buffer, so ``o.transpose(1, 2).reshape(B, S, -1)``
     (o_proj's input, model/attention.py:117) costs nothing.  With
     ``return_lse`` also returns the fp32 (B, Hq, S) log-sum-exp.  With
@@ -312,15 +362,33 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     pb = _i32(pos_base, dev)
     qw = _f32(q_weight, dev)
     st = _lib.strides3
-    args = (
-        _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
-        _ptr(out), st(out.stride()[:3]), _ptr(lse), _ptr(kl),
-        B, Hq, Hkv, S, T, D, dt, _ptr(qw), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
-        _ptr(pos), _ptr(pb), int(pos_offset), int(bool(causal)),
-        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
-    call = KernelCall(_lib.load().nq_attn_prefill_fwd, args, len(args) - 1, "nq_attn_prefill_fwd",
-                      (q, k, v, cos_t, sin_t, pos, pb, qw, kl), (out, lse) if return_lse else out)
+    head = (_ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
+            _ptr(out), st(out.stride()[:3]), _ptr(lse), _ptr(kl))
+    tail = (B, Hq, Hkv, S, T, D, dt, _ptr(qw), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
+            _ptr(pos), _ptr(pb), int(pos_offset), int(bool(causal)),
+            float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    keep = (q, k, v, cos_t, sin_t, pos, pb, qw, kl)
+    if bias is not None:
+        _check_bias(bias, B, Hq, S, T, q.dtype)
+        args = head + (_ptr(bias.bias), st(bias.strides)) + tail
+        call = KernelCall(_lib.load().nq_attn_prefill_bias_fwd, args, len(args) - 1, "nq_attn_prefill_bias_fwd",
+                          keep + (bias.bias,), (out, lse) if return_lse else out)
+    else:
+        args = head + tail
+        call = KernelCall(_lib.load().nq_attn_prefill_fwd, args, len(args) - 1, "nq_attn_prefill_fwd",
+                          keep, (out, lse) if return_lse else out)
     return call if plan else call.launch()
+
+
+def _check_bias(bias: AttnBias, B: int, Hq: int, S: int, T: int, dtype: torch.dtype, transpose: bool = False):
+    if not isinstance(bias, AttnBias):
+        raise TypeError("bias must be an AttnBias (build one from the attn_mask)")
+    if bias.shape != (B, Hq, S, T):
+        raise ValueError(f"the bias was built for (B, Hq, S, T) = {bias.shape}, the call has {(B, Hq, S, T)}")
+    if bias.bias.dtype != dtype:
+        raise TypeError(f"the bias holds {bias.bias.dtype}, the call computes in {dtype}")
+    if transpose and bias.bias_t is None:
+        raise ValueError("the backward needs the bias built with transpose=True")
 
 
 def attention_prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
@@ -660,13 +728,15 @@ def attention_merge_(o: torch.Tensor, lse: torch.Tensor, o_part: torch.Tensor,
 def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                        dout: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
                        sm_scale: Optional[float] = None, key_lens: Optional[torch.Tensor] = None,
+                       bias: Optional[AttnBias] = None,
                        workspace: Optional[torch.Tensor] = None, plan: bool = False):
-    """FlashAttention-2 backward: (dq, dk, dv) of o = softmax(scale q k^T) v.
+    """FlashAttention-2 backward: (dq, dk, dv) of o = softmax(scale q k^T + bias) v.
 
     q: (B, Hq, S, D), k/v: (B, Hkv, T, D) as the forward attended them (after
     QK-Norm and RoPE); o, dout: (B, Hq, S, D); lse: the forward's fp32
     (B, Hq, S) log-sum-exp (``attention_prefill(..., return_lse=True)`` with
-    the same causal, sm_scale and key_lens).  dk/dv sum the gradients of the
+    the same causal, sm_scale, key_lens and bias; the bias built with
+    ``transpose=True``).  dk/dv sum the gradients of the
     G query heads that share a kv head; keys past key_lens[b] get zeros.
     Returns fresh (dq, dk, dv) in q's dtype.
     """
@@ -694,15 +764,21 @@ def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: tor
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     st = _lib.strides3
-    args = (
-        _ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
-        _ptr(o), st(o.stride()[:3]), _ptr(dout), st(dout.stride()[:3]), _ptr(lse), _ptr(kl),
-        _ptr(dq), st(dq.stride()[:3]), _ptr(dk), st(dk.stride()[:3]), _ptr(dv), st(dv.stride()[:3]),
-        _ptr(workspace), workspace.numel() * workspace.element_size(),
-        B, Hq, Hkv, S, T, D, _code(q), int(bool(causal)),
-        float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
-    call = KernelCall(lib.nq_attn_bwd, args, len(args) - 1, "nq_attn_bwd",
-                      (q, k, v, o, dout, lse, workspace, kl), (dq, dk, dv))
+    head = (_ptr(q), st(q.stride()[:3]), _ptr(k), st(k.stride()[:3]), _ptr(v), st(v.stride()[:3]),
+            _ptr(o), st(o.stride()[:3]), _ptr(dout), st(dout.stride()[:3]), _ptr(lse), _ptr(kl))
+    tail = (_ptr(dq), st(dq.stride()[:3]), _ptr(dk), st(dk.stride()[:3]), _ptr(dv), st(dv.stride()[:3]),
+            _ptr(workspace), workspace.numel() * workspace.element_size(),
+            B, Hq, Hkv, S, T, D, _code(q), int(bool(causal)),
+            float(sm_scale) if sm_scale is not None else 0.0, _stream(q))
+    keep = (q, k, v, o, dout, lse, workspace, kl)
+    if bias is not None:
+        _check_bias(bias, B, Hq, S, T, q.dtype, transpose=True)
+        args = head + (_ptr(bias.bias), st(bias.strides), _ptr(bias.bias_t), st(bias.t_strides)) + tail
+        call = KernelCall(lib.nq_attn_bwd_bias, args, len(args) - 1, "nq_attn_bwd_bias",
+                          keep + (bias.bias, bias.bias_t), (dq, dk, dv))
+    else:
+        args = head + tail
+        call = KernelCall(lib.nq_attn_bwd, args, len(args) - 1, "nq_attn_bwd", keep, (dq, dk, dv))
     return call if plan else call.launch()
 
 
@@ -724,15 +800,20 @@ def qk_norm_rope_backward(x: torch.Tensor, dy: torch.Tensor, *, weight: Optional
     dev = x.device
     dx = torch.empty(B, S, H, D, dtype=x.dtype, device=dev).transpose(1, 2)
     w = _f32(weight, dev)
-    dw = torch.zeros(D, dtype=torch.float32, device=dev) if w is not None else None
+    lib = _lib.load()
+    dw, ws, wbytes = None, None, 0
+    if w is not None:
+        dw = torch.empty(D, dtype=torch.float32, device=dev)
+        wbytes = int(lib.nq_qk_norm_rope_bwd_workspace_bytes(B, S, H, D))
+        ws = torch.empty(wbytes, dtype=torch.uint8, device=dev)
     cos_t, sin_t, max_pos = _tables(cos, sin, dev)
     pos = _positions(position_ids, pos_offset, pos_base, B, S, max_pos, dev)
     pb = _i32(pos_base, dev)
     st = _lib.strides3
-    rc = _lib.load().nq_qk_norm_rope_bwd(
+    rc = lib.nq_qk_norm_rope_bwd(
         _ptr(x), st(x.stride()[:3]), _ptr(dy), st(dy.stride()[:3]), _ptr(dx), st(dx.stride()[:3]),
-        _ptr(w), _ptr(dw), B, S, H, D, _code(x), float(eps), _ptr(cos_t), _ptr(sin_t), max_pos,
-        _ptr(pos), _ptr(pb), int(pos_offset), _stream(x))
+        _ptr(w), _ptr(dw), _ptr(ws), wbytes, B, S, H, D, _code(x), float(eps), _ptr(cos_t), _ptr(sin_t),
+        max_pos, _ptr(pos), _ptr(pb), int(pos_offset), _stream(x))
     _lib.check(rc, "nq_qk_norm_rope_bwd")
     return dx, dw
 

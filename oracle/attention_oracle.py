@@ -209,7 +209,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
             else:
                 sc = sc + mb.to(compute_dtype)
         sc = sc.masked_fill(~keep, float("-inf"))
-        p = torch.softmax(sc, dim=-1)
+        # a row with every key masked (all scores -inf) attends nothing: zeros,
+        # as torch's SDPA returns (softmax alone would give NaN); its scores are
+        # made finite first so that no NaN reaches autograd either
+        none = torch.isneginf(sc).all(-1, keepdim=True)
+        p = torch.softmax(sc.masked_fill(none, 0.0), dim=-1).masked_fill(none, 0.0)
         out[:, :, s0:s1] = torch.matmul(p, vc)
     return out
 

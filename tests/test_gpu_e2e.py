@@ -271,3 +271,28 @@ def test_training_step_gradients_against_oracle(weights):
         assert float(d.max()) <= 1e-4 * scale and float(d.mean()) <= 1e-5 * scale, \
             f"{name}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {scale:.3e})"
     say(f"training step: loss rel err {abs(got_loss - ref_loss) / ref_loss:.2e}, worst grad rel err {worst:.2e}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gradient_checkpointing_gradients_bit_equal(weights, dtype):
+    """transformer.py:92,121-127: with gradient_checkpointing each block's forward
+    (the attention kernels' autograd Function included) runs again inside the
+    backward; the kernels are deterministic, so every parameter gradient equals
+    the one without recompute bit for bit."""
+    say(f"gradient checkpointing {dtype}")
+    g = torch.Generator().manual_seed(611)
+    ids = torch.randint(0, MODEL["vocab_size"], (2, 80), generator=g).cuda()
+    grads = {}
+    for ckpt in (False, True):
+        torch.manual_seed(0)
+        m = Qwen3Model(ModelConfig(**MODEL, gradient_checkpointing=ckpt)).train()
+        m.load_state_dict(weights, strict=True)
+        m = m.to("cuda", dtype)
+        assert m.gradient_checkpointing is ckpt
+        before = stats["kernel_train_forward"]
+        m(ids, labels=ids)["loss"].backward()
+        # the attention forward runs once per layer, and once more per layer under recompute
+        assert stats["kernel_train_forward"] == before + MODEL["num_hidden_layers"] * (2 if ckpt else 1)
+        grads[ckpt] = {n: p.grad.clone() for n, p in m.named_parameters()}
+    for n, gr in grads[False].items():
+        assert torch.equal(gr, grads[True][n]), n

@@ -1,11 +1,14 @@
-"""Key-padding masks on the kernels (model/attention.py:110-114 with attn_mask,
+"""Attention masks on the kernels (model/attention.py:110-114 with attn_mask,
 the reward model's padded batches, training/reward_model.py:45).
 
 A mask that keeps, for every head and query, the same prefix [0, L_b) of each
 sequence's keys runs the prefill (and, under autograd, the backward) kernels
-with per-sequence key counts; any other mask takes SDPA.  References: the
-oracle's attention with key_lens / the mask (fp32 math, fp64 for gradients).
-Padded K/V rows are poisoned with NaN: the kernels must never read them.
+with per-sequence key counts; any other bool or float mask runs them with an
+additive bias read per tile (ops.AttnBias).  No mask takes a torch path.
+References: the oracle's attention with key_lens / the mask (fp32 math, fp64
+for gradients; a row with every key masked gives zeros, as SDPA does, pinned
+against SDPA in the oracle tests).  Padded K/V rows are poisoned with NaN: the
+kernels must never read them.
 """
 
 import pytest
@@ -13,7 +16,7 @@ import torch
 
 import nano_qwen_amd as nq
 from nano_qwen_amd import ops
-from oracle import attention, attention_module_forward, rope_tables
+from oracle import OracleKVCache, attention, attention_module_forward, rope_tables
 from tests.helpers import assert_bf16_close, assert_close_for, randn, say
 
 pytestmark = pytest.mark.gpu
@@ -180,24 +183,139 @@ def test_module_key_padding_mask_runs_the_kernels(dtype, kind):
 
 
 @torch.no_grad()
-def test_module_other_masks_take_sdpa():
-    """Left padding (a hole before the kept keys), a query-dependent mask and an
-    additive bias are not key-padding prefixes: they run SDPA, as the reference."""
-    say("module non-prefix masks -> SDPA")
-    attn, w = _module(torch.float32)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_module_other_masks_run_the_bias_kernels(dtype):
+    """Left padding (a hole before the kept keys), a query-dependent mask, an
+    additive bias and a per-head mask are not key-padding prefixes: they run the
+    kernels with the mask as a per-tile bias, and match the oracle module."""
+    say(f"module non-prefix masks -> bias kernels {dtype}")
+    attn, w = _module(dtype)
     B, S = 2, 32
-    h = randn(B, S, 256, seed=741)
+    h = randn(B, S, 256, seed=741, dtype=dtype)
     cos, sin = rope_tables(64, 512, 1e6)
     left = (torch.arange(S)[None, :] >= torch.tensor([0, 5])[:, None])[:, None, None, :]
     causal = torch.ones(S, S, dtype=torch.bool).tril()
-    bias = 0.1 * randn(1, 1, 1, S, seed=742)
-    for mask in (left, causal, bias):
-        before = nq.stats["torch_forward"]
+    bias = (0.1 * randn(1, 1, 1, S, seed=742)).to(dtype)
+    heads = torch.rand(1, 8, S, S, generator=torch.Generator().manual_seed(743)) > 0.5
+    heads[..., 0] = True
+    for mask in (left, causal, bias, heads):
+        before = dict(nq.stats)
         out = attn(h.to(DEV), attention_mask=mask.to(DEV))
-        assert nq.stats["torch_forward"] == before + 1
-        ref, _ = attention_module_forward(h, w, num_heads=8, num_kv_heads=2, head_dim=64, eps=1e-6,
-                                          cos_table=cos, sin_table=sin, attention_mask=mask)
-        assert_close_for(torch.float32, out, ref, "sdpa path")
+        assert nq.stats["torch_forward"] == before["torch_forward"] == 0
+        assert nq.stats["kernel_forward"] == before["kernel_forward"] + 1
+        ref, _ = attention_module_forward(h, {k: v.to(dtype) for k, v in w.items()}, num_heads=8, num_kv_heads=2,
+                                          head_dim=64, eps=1e-6, cos_table=cos, sin_table=sin, attention_mask=mask)
+        if dtype == torch.float32:
+            assert_close_for(dtype, out, ref, "bias kernels")
+        else:
+            assert_bf16_close(out, ref, "bias kernels", max_abs=3e-2)
+
+
+def _bias_masks(kind, B, Hq, S, T, dtype, seed):
+    """Masks broadcastable to (B, Hq, S, T): bool keep-masks (with fully masked rows)
+    and float biases (with -inf entries and large finite offsets)."""
+    g = torch.Generator().manual_seed(seed)
+    if kind == "bool":
+        m = torch.rand(B, 1, S, T, generator=g) > 0.35
+        m[0, 0, 5] = False                                   # a row with no key at all
+        m[-1, 0, :, :70] = False                             # rows whose first tile(s) are all masked
+        return m
+    if kind == "float":
+        m = 0.5 * torch.randn(B, 1, S, T, generator=g)
+        m = m.masked_fill(torch.rand(B, 1, S, T, generator=g) < 0.3, float("-inf"))
+        m[0, 0, 7] = float("-inf")
+        return m.to(dtype)
+    if kind == "heads":                                      # per-head, broadcast over the batch
+        m = torch.rand(1, Hq, S, T, generator=g) > 0.5
+        m[0, 1, :, :] = False
+        return m
+    if kind == "far":
+        # the first 64+ keys masked, the rest far below zero: the running max
+        # must start from the first finite tile, not from a placeholder
+        m = torch.full((B, 1, S, T), -30000.0) + torch.randn(B, 1, S, T, generator=g)
+        m[..., :80] = float("-inf")
+        return m.to(dtype)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kind", ["bool", "float", "heads", "far"])
+def test_prefill_bias(dtype, D, kind):
+    say(f"prefill bias {kind} {dtype} D={D}")
+    B, Hq, Hkv, S, T = 2, 8, 2, 150, 150
+    q = randn(B, Hq, S, D, seed=761, dtype=dtype)
+    k = randn(B, Hkv, T, D, seed=762, dtype=dtype)
+    v = randn(B, Hkv, T, D, seed=763, dtype=dtype)
+    mask = _bias_masks(kind, B, Hq, S, T, dtype, 764)
+    bias = ops.AttnBias(mask.to(DEV), B, Hq, S, T, dtype, DEV)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=False, bias=bias, return_lse=True)
+    assert torch.isfinite(o.float()).all()
+    if kind == "far" and dtype == torch.float32:
+        # every finite logit is about -4.3e4 in log2 units, where fp32 spacing is
+        # 2^-8: any fp32 evaluation (the reference's too) moves P by ~0.5%, so the
+        # gate is against fp64 at that level (a wrong running max gives zeros)
+        ref = attention(q.double(), k.double(), v.double(), mask=mask.double(), compute_dtype=torch.float64)
+        d = (o.double().cpu() - ref).abs()
+        assert float(d.max()) <= 1e-2 and float(d.mean()) <= 1e-3, (float(d.max()), float(d.mean()))
+    else:
+        ref = attention(q.float(), k.float(), v.float(), mask=mask if mask.dtype == torch.bool else mask.float())
+        assert_close_for(dtype, o, ref, f"bias {kind}")
+    sc = torch.matmul(q.float(), k.float().repeat_interleave(Hq // Hkv, 1).transpose(-1, -2)) / D ** 0.5
+    sc = sc.masked_fill(~mask, float("-inf")) if mask.dtype == torch.bool else sc + mask.float()
+    want = torch.logsumexp(sc, -1)
+    got = lse.cpu()
+    assert torch.equal(torch.isneginf(got), torch.isneginf(want))
+    fin = torch.isfinite(want)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(got[fin], want[fin], rtol=1e-5, atol=tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_bias_with_causal_and_key_lens(dtype):
+    """A bias together with the causal frontier (T > S, bottom-right) and key padding."""
+    say(f"prefill bias + causal + key_lens {dtype}")
+    B, Hq, Hkv, S, T, D = 3, 8, 4, 100, 140, 128
+    lens = torch.tensor([140, 60, 121], dtype=torch.int32)
+    q = randn(B, Hq, S, D, seed=771, dtype=dtype)
+    k = _poison(randn(B, Hkv, T, D, seed=772, dtype=dtype), lens)
+    v = _poison(randn(B, Hkv, T, D, seed=773, dtype=dtype), lens)
+    mask = (0.3 * randn(B, 1, S, T, seed=774)).to(dtype)
+    bias = ops.AttnBias(mask.to(DEV), B, Hq, S, T, dtype, DEV)
+    o = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, bias=bias, key_lens=lens.to(DEV))
+    ref = attention(q.float(), k.float().nan_to_num(), v.float().nan_to_num(), causal=True, causal_offset=T - S,
+                    key_lens=lens, mask=mask.float())
+    assert_close_for(dtype, o, ref, "bias + causal + key_lens")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("kind", ["bool", "float"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_bias(dtype, kind, causal):
+    """Gradients with a general mask against fp64 autograd of the oracle (rows whose keys
+    are all masked get zero dQ and contribute nothing to dK, dV)."""
+    say(f"backward bias {kind} {dtype} causal={causal}")
+    B, Hq, Hkv, S, D = 2, 8, 2, 130, 128
+    q = randn(B, Hq, S, D, seed=781, dtype=dtype)
+    k = randn(B, Hkv, S, D, seed=782, dtype=dtype)
+    v = randn(B, Hkv, S, D, seed=783, dtype=dtype)
+    do = randn(B, Hq, S, D, seed=784, dtype=dtype)
+    mask = _bias_masks(kind, B, Hq, S, S, dtype, 785)
+    bias = ops.AttnBias(mask.to(DEV), B, Hq, S, S, dtype, DEV, transpose=True)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, bias=bias, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=causal,
+                                        bias=bias)
+    qd, kd, vd = (t.double().requires_grad_(True) for t in (q, k, v))
+    md = mask if mask.dtype == torch.bool else mask.double()
+    attention(qd, kd, vd, causal=causal, mask=md, compute_dtype=torch.float64).backward(do.double())
+    mx_tol, mean_tol = (1e-5, 1e-6) if dtype == torch.float32 else (2e-2, 2e-3)
+    for got, ref, name in ((dq, qd.grad, "dq"), (dk, kd.grad, "dk"), (dv, vd.grad, "dv")):
+        got = got.double().cpu()
+        assert torch.isfinite(got).all(), name
+        sc = float(ref.abs().max())
+        d = (got - ref).abs()
+        assert float(d.max()) <= mx_tol * sc and float(d.mean()) <= mean_tol * sc, \
+            f"{name}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {sc:.3e})"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -228,3 +346,102 @@ def test_module_training_with_key_padding(dtype):
         d = (got - t.grad).abs()
         assert float(d.max()) <= mx_tol * sc and float(d.mean()) <= mean_tol * sc, \
             f"grad {n}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {sc:.3e})"
+
+
+def _grad_close(got, ref, name, dtype):
+    """fp64-autograd comparison, relative to the reference's largest magnitude: the
+    fp32 gate 1e-5 / 1e-6 (max / mean), the bf16 module's 5e-2 / 5e-3."""
+    mx_tol, mean_tol = (1e-5, 1e-6) if dtype == torch.float32 else (5e-2, 5e-3)
+    got = got.double().cpu()
+    assert torch.isfinite(got).all(), name
+    sc = float(ref.abs().max())
+    d = (got - ref).abs()
+    assert float(d.max()) <= mx_tol * sc and float(d.mean()) <= mean_tol * sc, \
+        f"{name}: max-abs {float(d.max()):.3e} mean-abs {float(d.mean()):.3e} (ref max {sc:.3e})"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_module_training_with_general_mask(dtype):
+    """A non-prefix mask under autograd: forward and backward on the bias kernels,
+    every weight gradient against fp64 autograd of the oracle module."""
+    say(f"module training with a general mask {dtype}")
+    attn, w = _module(dtype, seed=791)
+    attn.train()
+    B, S = 2, 70
+    g = torch.Generator().manual_seed(792)
+    mask = torch.rand(B, 1, S, S, generator=g) > 0.3
+    mask |= torch.eye(S, dtype=torch.bool)
+    h = randn(B, S, 256, seed=793, dtype=dtype)
+    gout = randn(B, S, 256, seed=794, dtype=dtype)
+    before = dict(nq.stats)
+    out = attn(h.to(DEV), attention_mask=mask.to(DEV))
+    out.backward(gout.to(DEV))
+    assert nq.stats["kernel_train_forward"] == before["kernel_train_forward"] + 1
+    assert nq.stats["torch_forward"] == 0
+    cos, sin = rope_tables(64, 512, 1e6)
+    wd = {k: v.double().requires_grad_(True) for k, v in w.items()}
+    ref, _ = attention_module_forward(h.double(), wd, num_heads=8, num_kv_heads=2, head_dim=64, eps=1e-6,
+                                      cos_table=cos.double(), sin_table=sin.double(), attention_mask=mask)
+    ref.backward(gout.double())
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm"):
+        _grad_close(getattr(attn, name).weight.grad, wd[name].grad, name, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_module_autograd_through_a_kv_cache(dtype):
+    """Autograd with a KVCache (attention.py:102-115): a prompt cached without grad, then a
+    continuation under autograd that appends its rows and attends every cached row.  The
+    forward matches the oracle module with the reference's concatenating cache, and so do
+    the gradients of every weight and of the continuation's hidden states."""
+    say(f"module autograd through a KV cache {dtype}")
+    attn, w = _module(dtype, seed=801)
+    attn.train()
+    B, S0, S1 = 2, 40, 17
+    h0 = randn(B, S0, 256, seed=802, dtype=dtype)
+    h1 = randn(B, S1, 256, seed=803, dtype=dtype)
+    gout = randn(B, S1, 256, seed=804, dtype=dtype)
+    cache = nq.KVCache()
+    with torch.no_grad():
+        attn(h0.to(DEV), kv_cache=cache)
+    x1 = h1.to(DEV).requires_grad_(True)
+    before = dict(nq.stats)
+    out = attn(x1, kv_cache=cache)
+    out.backward(gout.to(DEV))
+    assert nq.stats["kernel_train_forward"] == before["kernel_train_forward"] + 1
+    assert nq.stats["torch_forward"] == 0
+    assert cache.seq_len == S0 + S1
+    cos, sin = rope_tables(64, 512, 1e6)
+    wd = {k: v.double().requires_grad_(True) for k, v in w.items()}
+    oc = OracleKVCache()
+    with torch.no_grad():
+        attention_module_forward(h0.double(), {k: v.detach() for k, v in wd.items()}, num_heads=8,
+                                 num_kv_heads=2, head_dim=64, eps=1e-6, cos_table=cos.double(),
+                                 sin_table=sin.double(), kv_cache=oc)
+    x1r = h1.double().requires_grad_(True)
+    ref, _ = attention_module_forward(x1r, wd, num_heads=8, num_kv_heads=2, head_dim=64, eps=1e-6,
+                                      cos_table=cos.double(), sin_table=sin.double(), kv_cache=oc)
+    ref.backward(gout.double())
+    _grad_close(out.detach(), ref.detach(), "output", dtype)
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm"):
+        _grad_close(getattr(attn, name).weight.grad, wd[name].grad, name, dtype)
+    _grad_close(x1.grad, x1r.grad, "hidden", dtype)
+
+
+def test_attention_dropout_raises_while_training():
+    """attention.py:114 applies dropout_p while training; the kernels have none, so a
+    config with attention_dropout > 0 is refused in training mode (no reference config
+    sets it) and runs the kernels in eval mode."""
+    say("attention dropout: refused while training")
+    cfg = nq.AttentionConfig(hidden_size=256, num_attention_heads=8, num_key_value_heads=2, head_dim=64,
+                             max_position_embeddings=512, attention_dropout=0.1)
+    attn = nq.Attention(cfg).to(DEV)
+    h = randn(2, 16, 256, seed=811).to(DEV)
+    attn.train()
+    with pytest.raises(NotImplementedError, match="dropout"):
+        attn(h)
+    attn.eval()
+    before = dict(nq.stats)
+    with torch.no_grad():
+        out = attn(h)
+    assert torch.isfinite(out).all()
+    assert nq.stats["kernel_forward"] == before["kernel_forward"] + 1 and nq.stats["torch_forward"] == 0

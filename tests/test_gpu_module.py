@@ -103,13 +103,15 @@ def test_bf16_module_matches_reference(fx):
 
 
 @torch.no_grad()
-def test_mask_takes_torch_path_and_matches(fx):
-    say("module mask (torch path)")
+def test_mask_runs_the_bias_kernels_and_matches(fx):
+    """The reference's own outputs for a random (B, 1, S, S) bool mask: the kernels
+    with the mask as a per-tile bias."""
+    say("module mask (bias kernels)")
     attn, h = _module()
     box = _capture(attn)
-    before = nq.stats["torch_forward"]
+    before = dict(nq.stats)
     out = attn(h, attention_mask=torch.from_numpy(fx["mask_mask"]).to(DEV))
-    assert nq.stats["torch_forward"] == before + 1
+    assert nq.stats["kernel_forward"] == before["kernel_forward"] + 1 and nq.stats["torch_forward"] == 0
     np.testing.assert_allclose(box["attn"].cpu().numpy(), fx["mask_attn"], rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(out.cpu().numpy(), fx["mask_out"], rtol=1e-4, atol=1e-4)
 

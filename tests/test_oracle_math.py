@@ -305,3 +305,27 @@ def test_reference_chunk_sdpa_equals_attention_path():
     torch.testing.assert_close(o, br, rtol=1e-5, atol=1e-6)
     tl = attention_path(q[:, :, T0:], k, v, causal_offset=0, **kw_args)  # top-left frontier
     assert not torch.allclose(tl, o, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("kind", ["bool", "float"])
+def test_attention_masks_against_sdpa(kind):
+    """The oracle's attn_mask handling (model/attention.py:110-113) against torch's SDPA,
+    the library routine the reference calls: a bool keep-mask or an additive float mask,
+    broadcast over heads, with rows whose keys are all masked (SDPA returns zeros there),
+    in GQA form against SDPA over the repeat_interleave'd heads."""
+    import torch.nn.functional as F
+    B, Hq, Hkv, S, T, D = 2, 4, 2, 9, 13, 16
+    q, k, v = _rand(B, Hq, S, D, seed=91), _rand(B, Hkv, T, D, seed=92), _rand(B, Hkv, T, D, seed=93)
+    g = torch.Generator().manual_seed(94)
+    keep = torch.rand(B, 1, S, T, generator=g) > 0.4
+    keep[0, 0, 3] = False            # a fully masked row
+    keep[1, 0, :, 0] = False
+    if kind == "bool":
+        mask = keep
+    else:
+        mask = torch.zeros(B, 1, S, T, dtype=torch.float64).masked_fill(~keep, float("-inf"))
+        mask = mask + 0.3 * torch.randn(B, 1, S, T, generator=g, dtype=torch.float64)
+    got = attention(q, k, v, mask=mask, compute_dtype=torch.float64)
+    ref = F.scaled_dot_product_attention(q, k.repeat_interleave(2, 1), v.repeat_interleave(2, 1), attn_mask=mask)
+    torch.testing.assert_close(got, ref, rtol=1e-10, atol=1e-10)
+    assert not got[0, :, 3].abs().any()
