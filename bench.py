@@ -35,7 +35,10 @@ as B=1 slices with their own lengths, C5 as one KV group of four (the
 extrapolation stated in ``sample``).  A sample shorter than CPU_MIN_S is
 repeated in whole passes (``passes``).
 ``cores`` is the number of threads torch used; ``host_cpu_count`` is
-os.cpu_count().  ``roofline.traffic`` is profile-derived (``traffic_source``).
+os.cpu_count().  ``roofline.traffic`` is profile-derived (``traffic_source``);
+``roofline.traffic_ratio`` divides it by the kernel's compulsory HBM bytes
+(prefill: Q, K, V in and O out; decode: the cache rows once, Q, O; backward:
+Q, K, V, O, dO in and dQ, dK, dV out).
 """
 
 from __future__ import annotations
@@ -89,6 +92,8 @@ class Prefill:
         self.khat = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
         self.out = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
         self.work = 4.0 * D * B * Hq * S * (S + 1) / 2
+        # compulsory HBM bytes of the kernel: Q in and O out, K-hat and V in
+        self.algo_bytes = 2 * B * S * (Hq + Hkv) * D * 2
         self.rope_scaling = rope_scaling
 
         # validated, pre-bound launches: one foreign call each per step
@@ -145,6 +150,7 @@ class Decode:
         nbytes = nq.decode_workspace_bytes(B, Hq, Hkv, D, self.max_len)
         self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         self.work = float(2 * Hkv * D * 2 * int(self.lens_cpu.sum()) + 2 * B * Hq * D * 2)
+        self.algo_bytes = self.work
 
         self.a_call = nq.qk_norm_rope(k=self.knew, v=self.vnew, k_out=self.kc, v_out=self.vc,
                                       k_weight=self.w, eps=1e-6, cos=self.cos, sin=self.sin,
@@ -207,6 +213,7 @@ class PagedDecode(Decode):
         nbytes = nq.decode_workspace_bytes(B, Hq, Hkv, D, self.max_len)
         self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         self.work = float(2 * Hkv * D * 2 * int(self.lens_cpu.sum()) + 2 * B * Hq * D * 2)
+        self.algo_bytes = self.work
         self.d_call = nq.attention_decode_paged(
             self.q, self.kp, self.vp, self.bt, self.held, max_len=self.max_len, k_new=self.knew,
             v_new=self.vnew, k_weight=self.w, lens_out=self.lens_out, q_weight=self.w, eps=1e-6,
@@ -253,6 +260,7 @@ class PagedChunk:
         self.vp = torch.randn(B * npp, Hkv, page, D, generator=gd, device=device, dtype=torch.bfloat16)
         self.out = torch.empty(B, C, Hq, D, dtype=torch.bfloat16, device=device).transpose(1, 2)
         self.work = 4.0 * D * B * Hq * (C * self.p0 + C * (C + 1) / 2)
+        self.algo_bytes = 2 * B * C * Hq * D * 2 + 2 * B * T * Hkv * D * 2  # Q, O; all T keys' K-hat, V
         self.a_call = nq.kv_append_paged(self.k, self.v, self.kp, self.vp, self.bt, k_weight=self.kw,
                                          eps=1e-6, cos=self.cos, sin=self.sin, row_offset=self.p0,
                                          pos_offset=self.p0, plan=True)
@@ -301,6 +309,8 @@ class Backward:
         self.o, self.lse = nq.attention_prefill(self.q, self.k, self.v, causal=True, return_lse=True)
         # FlashAttention-2 convention: 5 matrix products over the causal pairs
         self.work = 2.5 * 4.0 * D * B * Hq * S * (S + 1) / 2
+        # Q, O, dO in and dQ out; K, V in and dK, dV out
+        self.algo_bytes = 4 * B * S * (Hq + Hkv) * D * 2
         self.call = nq.ops.attention_backward(self.q, self.k, self.v, self.o, self.do, self.lse,
                                               causal=True, plan=True)
 
@@ -649,7 +659,7 @@ def main():
         results[name] = {"config": w.describe(), "value": round(val, 3), "unit": unit,
                          "ms_per_step": round(step_ms, 5), "steps": steps, "warmup": warm,
                          "settle_steps": n_settle,
-                         "roofline": w.roofline(kern_ms)}
+                         "roofline": w.roofline(kern_ms), "_algo_bytes": w.algo_bytes}
         log(f"{name}: {step_ms:.4f} ms/step, kernel avg {kern_ms:.4f} ms, {val:.2f} {unit}")
         if not args.no_cpu_baseline:
             log(f"{name}: cpu baseline (the reference's composition in fp32 on the host cores)")
@@ -663,6 +673,9 @@ def main():
     for name, r in results.items():
         r["roofline"]["traffic"] = traffic.get(name)
         r["roofline"]["traffic_source"] = TRAFFIC_SOURCE if name in traffic else None
+        # counter bytes over the kernel's compulsory bytes (1.0: every byte crosses HBM once)
+        algo = r.pop("_algo_bytes")
+        r["roofline"]["traffic_ratio"] = round(traffic[name] / algo, 2) if name in traffic else None
         if name == "c4_paged" and "c4" in cpu:
             r["cpu_baseline"] = dict(cpu["c4"], sample="the c4 sequences (the reference has no "
                                      "paged cache): " + cpu["c4"]["sample"])

@@ -90,7 +90,8 @@ def test_decode_equals_last_row_of_prefill():
 
 def test_qwen3_235b_decode_full_size():
     """B64, Hq64/Hkv4, D128, lens ~ U[1024, 32768], T_cap 32768; tails poisoned with NaN;
-    every row against the oracle."""
+    every row against the oracle, with the query's QK-Norm (weights 1 + 0.02 N(0,1)) and
+    RoPE fused into its load, as the bench's decode step runs it."""
     say("decode Qwen3-235B-A22B B64 T_cap 32768")
     B, Hq, Hkv, D, Tcap = 64, 64, 4, 128, 32768
     g = torch.Generator().manual_seed(1003)
@@ -102,14 +103,15 @@ def test_qwen3_235b_decode_full_size():
         kc[b, :, lens[b]:] = float("nan")
         vc[b, :, lens[b]:] = float("nan")
     q = randn(B, Hq, D, seed=1005, dtype=torch.bfloat16)
+    qw = 1 + 0.02 * randn(D, seed=1006)
     cos, sin = rope_tables(D, Tcap, 1e6)
     ld = lens.to(DEV)
-    o = nq.attention_decode(q.to(DEV), kc, vc, ld, max_len=int(lens.max()), cos=cos.to(DEV),
-                            sin=sin.to(DEV)).cpu()
+    o = nq.attention_decode(q.to(DEV), kc, vc, ld, max_len=int(lens.max()), q_weight=qw.to(DEV), eps=1e-6,
+                            cos=cos.to(DEV), sin=sin.to(DEV)).cpu()
     assert torch.isfinite(o.float()).all()
     for b in range(B):  # every row, the shortest and the longest among them
         L = int(lens[b])
         ref = decode_path(q[b:b + 1].float(), kc[b:b + 1, :, :L].float().cpu(),
-                          vc[b:b + 1, :, :L].float().cpu(), lens[b:b + 1], q_weight=None,
+                          vc[b:b + 1, :, :L].float().cpu(), lens[b:b + 1], q_weight=qw,
                           eps=1e-6, cos=cos, sin=sin, q_pos=lens[b:b + 1].long() - 1)
         assert_bf16_close(o[b:b + 1], ref, f"235B b={b} len={L}")
