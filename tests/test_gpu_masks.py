@@ -445,3 +445,26 @@ def test_attention_dropout_raises_while_training():
         out = attn(h)
     assert torch.isfinite(out).all()
     assert nq.stats["kernel_forward"] == before["kernel_forward"] + 1 and nq.stats["torch_forward"] == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D,Hq,Hkv", [(32, 8, 1), (64, 16, 1), (128, 4, 4)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_bias_shapes(dtype, D, Hq, Hkv, causal):
+    """The bias kernels at head_dim 32/64/128 and GQA groups 1, 8 and 16, with S < T
+    (a continuation over cached keys, bottom-right causal) and a per-head float bias
+    with -inf entries; a query-independent bias broadcast over heads too."""
+    say(f"prefill bias shapes {dtype} D={D} {Hq}/{Hkv} causal={causal}")
+    B, S, T = 2, 70, 201
+    q = randn(B, Hq, S, D, seed=911, dtype=dtype)
+    k = randn(B, Hkv, T, D, seed=912, dtype=dtype)
+    v = randn(B, Hkv, T, D, seed=913, dtype=dtype)
+    mask = 0.5 * randn(B, Hq, S, T, seed=914)
+    drop = torch.rand(B, Hq, S, T, generator=torch.Generator().manual_seed(915)) < 0.3
+    drop[..., 0] = False  # key 0 always kept: no row is masked entirely
+    mask = mask.masked_fill(drop, float("-inf")).to(dtype)
+    for m in (mask, mask[:, :1, :1].expand(B, 1, 1, T).contiguous()):
+        bias = ops.AttnBias(m.to(DEV), B, Hq, S, T, dtype, DEV)
+        o = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, bias=bias)
+        ref = attention(q.float(), k.float(), v.float(), causal=causal, causal_offset=T - S, mask=m.float())
+        assert_close_for(dtype, o, ref, f"bias {tuple(m.shape)}")

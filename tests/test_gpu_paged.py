@@ -390,3 +390,31 @@ def test_paged_chunked_prefill_full_size():
         qh = rotate_half(rms_norm(q[:, :, rows].float(), qw, 1e-6), cos[rows][None, None], sin[rows][None, None])
         ref = attention(qh, kh[:, :, :p0 + C], v[:, :, :p0 + C].float(), causal=True, causal_offset=p0 + s0)
         assert_bf16_close(outs[c][:, :, s0:s0 + 64], ref, f"chunk {c} rows {s0}..{s0 + 63} vs oracle")
+
+
+@pytest.mark.parametrize("dtype,D,P,Hq,Hkv", [
+    (torch.bfloat16, 128, 64, 8, 2), (torch.bfloat16, 128, 32, 16, 1), (torch.bfloat16, 64, 128, 4, 4),
+    (torch.bfloat16, 32, 32, 8, 1), (torch.float32, 128, 64, 8, 2), (torch.float32, 64, 32, 4, 1)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_paged_equals_dense(dtype, D, P, Hq, Hkv, causal):
+    """A chunk of S queries over T keys held in shuffled pages (T a multiple of neither
+    64 nor the page size; unmapped pages NaN): bit-identical to the dense kernel over the
+    same K-hat/V rows, and within the gate of the oracle."""
+    say(f"paged prefill {dtype} D={D} P={P} {Hq}/{Hkv} causal={causal}")
+    B, S, T = 3, 77, 213
+    q = randn(B, Hq, S, D, seed=901, dtype=dtype)
+    k = randn(B, Hkv, T, D, seed=902, dtype=dtype)
+    v = randn(B, Hkv, T, D, seed=903, dtype=dtype)
+    qw = 1 + 0.02 * randn(D, seed=904)
+    cos, sin = rope_tables(D, 512, 1e6)
+    kp, vp, bt = _pages(k, v, [T] * B, P, seed=905)
+    kw = dict(q_weight=qw.to(DEV), eps=1e-6, cos=cos.to(DEV), sin=sin.to(DEV), causal=causal, pos_offset=T - S)
+    got = ops.attention_prefill_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV), T=T, **kw)
+    want = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, want), float((got.float() - want.float()).abs().max())
+    rows = torch.arange(T - S, T)
+    qh = rotate_half(rms_norm(q.float(), qw, 1e-6), cos[rows][None, None], sin[rows][None, None])
+    ref = attention(qh, k.float(), v.float(), causal=causal, causal_offset=T - S)
+    assert_close_for(dtype, got, ref, "paged prefill vs oracle")
