@@ -17,9 +17,10 @@
 // heads of one position adjacent when the source stores them so (a wave then
 // reads contiguous memory and its rows share their cos/sin table rows, which
 // matters when the tables outgrow the L2), else position-fastest.  The grid
-// is capped at 16 blocks per CU and loops over rows, one row per thread per
-// pass.  HBM-bound: one read and one write per element; the weight and table
-// reads hit the caches.
+// is persistent (as many blocks as stay resident) and loops over rows, one
+// row per thread per pass; the weight and each row's table chunks reach the
+// lanes through LDS by DMA.  HBM-bound: one read and one write per element;
+// the weight and table reads hit the caches.
 
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
@@ -60,83 +61,149 @@ struct RowParams {
   int page_size;
 };
 
-// Grid cap: 16 blocks per CU on 256 CUs, one row per thread per pass.  Fewer,
-// longer-lived threads holding two rows each (four row loads in flight) measured
-// 3-6% slower than this at the 1.7B-like, 8B-like and YaRN K-hat shapes.
-constexpr int ROW_MAX_BLOCKS = 4096;
+// An opaque zero (a VALU move the compiler cannot see through): added to the
+// addresses of the per-row LDS reads so they stay inside the row loop;
+// hoisted, the weight reads would hold 16 registers across every row's wait.
+__device__ __forceinline__ int row_opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
 
-template <typename TI, typename TO, int D, int ROW_UNROLL>
+// LDS per wave: the norm weight (D fp32, staged once, 1 KiB slot), then the
+// lanes' table chunks (cos lo / cos hi / sin lo / sin hi, 16 bytes per lane
+// each: 4 KiB), refilled every row.
+constexpr int ROW_WAVE_LDS = 5 * 1024;
+
+// A persistent grid: as many blocks as stay resident (the occupancy of the
+// instance times the CUs), each looping over rows, one row per thread per
+// pass.  Per row a thread issues its two 16-byte row loads, then its table
+// chunks as DMA into its wave's LDS slice, and waits once: the row and table
+// latencies overlap, and the tables (and the weights) occupy no registers
+// while in flight, which keeps the kernel at 7-8 waves per SIMD.
+template <typename TI, typename TO, int D>
 __global__ __launch_bounds__(256) void norm_rope_rows_kernel(RowParams p) {
   constexpr int LPR = D / 16;         // lanes per row
   constexpr int RPW = 64 / LPR;       // rows per wave
-  constexpr int RPB = RPW * 4;        // rows per 256-thread block and unroll step
+  constexpr int RPB = RPW * 4;        // rows per 256-thread block
   static_assert(LPR == 2 || LPR == 4 || LPR == 8, "D must be 32, 64 or 128");
+  static_assert(D * 4 <= 1024, "the weight fits its 1 KiB slot");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * ROW_WAVE_LDS];
   const RowJob& jb = p.job[blockIdx.y];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane % LPR;         // chunk pair: [8sub, 8sub+8) and [D/2 + 8sub, ...)
+  unsigned char* const wslot = smem + wave * ROW_WAVE_LDS;  // weight
+  unsigned char* const tslot = wslot + 1024;                // table chunks
   const int64_t nrows = (int64_t)p.B * jb.H * p.S;
-  floatx8 w1{}, w2{};
-  if (jb.norm) {
-    w1 = Vec8<float>::load_f32(jb.weight + sub * 8);
-    w2 = Vec8<float>::load_f32(jb.weight + D / 2 + sub * 8);
-  }
-  for (int64_t row0 = (int64_t)blockIdx.x * RPB * ROW_UNROLL + wave * RPW + lane / LPR; row0 < nrows;
-       row0 += (int64_t)gridDim.x * RPB * ROW_UNROLL) {
-  int bb[ROW_UNROLL], ss_[ROW_UNROLL], hh[ROW_UNROLL];
-  bool act[ROW_UNROLL];
-  floatx8 x1[ROW_UNROLL], x2[ROW_UNROLL];
-#pragma unroll
-  for (int u = 0; u < ROW_UNROLL; ++u) {
-    const int64_t row = row0 + u * RPB;
-    act[u] = row < nrows;
-    // row -> (b, h, s): s fastest, or h fastest when the heads of one position
-    // are adjacent in memory (the projections' (B, S, H, D) storage): a wave
-    // then reads contiguous bytes and its rows share table rows
-    const uint32_t rr = act[u] ? (uint32_t)row : 0u;
-    if (jb.heads_inner) {
-      hh[u] = (int)(rr % (uint32_t)jb.H);
-      const uint32_t t = rr / (uint32_t)jb.H;
-      ss_[u] = (int)(t % (uint32_t)p.S);
-      bb[u] = (int)(t / (uint32_t)p.S);
-    } else {
-      ss_[u] = (int)(rr % (uint32_t)p.S);
-      const uint32_t t = rr / (uint32_t)p.S;
-      hh[u] = (int)(t % (uint32_t)jb.H);
-      bb[u] = (int)(t / (uint32_t)jb.H);
-    }
-    const TI* src = reinterpret_cast<const TI*>(jb.src) + bb[u] * jb.sb + hh[u] * jb.sh + ss_[u] * jb.ss + sub * 8;
-    x1[u] = act[u] ? Vec8<TI>::load_f32(src) : floatx8{};
-    x2[u] = act[u] ? Vec8<TI>::load_f32(src + D / 2) : floatx8{};
-  }
-#pragma unroll
-  for (int u = 0; u < ROW_UNROLL; ++u) {
-    const int pos = jb.rope ? table_row(row_position(p.pos, p.pos_base, p.pos0, bb[u], ss_[u], p.S), p.max_pos) : 0;
-    norm_rope_row<D>(x1[u], x2[u], jb.norm ? &w1 : nullptr, &w2, p.eps, jb.rope ? p.cos_tab : nullptr,
-                     p.sin_tab, pos, sub);
-    if (act[u]) {
-      const int s = ss_[u];
-      const int drow = jb.use_row_base ? ((p.row_base ? p.row_base[bb[u]] : p.row0) + s) : s;
-      int64_t slab = bb[u], prow = drow;
+  // lane l stages weight values [4 (l % (D/4)), +4): the slot holds the
+  // weight (repeated for D < 256); waited for with the first row
+  if (jb.norm) global_load_lds16(jb.weight + (lane % (D / 4)) * 4, wslot);
+  // explicit or per-batch positions need a load before the table row is known;
+  // the plain pos0 + s form needs none (a separate loop, so no merged path
+  // waits on a position load that was never issued)
+  auto rows = [&](auto pos_arrays) {
+    constexpr bool PA = decltype(pos_arrays)::value;
+    for (int64_t row = (int64_t)blockIdx.x * RPB + wave * RPW + lane / LPR; row < nrows;
+         row += (int64_t)gridDim.x * RPB) {
+      // row -> (b, h, s): s fastest, or h fastest when the heads of one
+      // position are adjacent in memory (the projections' (B, S, H, D)
+      // storage): a wave then reads contiguous bytes and its rows share table rows
+      const uint32_t rr = (uint32_t)row;
+      int b, h, s;
+      if (jb.heads_inner) {
+        h = (int)(rr % (uint32_t)jb.H);
+        const uint32_t t = rr / (uint32_t)jb.H;
+        s = (int)(t % (uint32_t)p.S);
+        b = (int)(t / (uint32_t)p.S);
+      } else {
+        s = (int)(rr % (uint32_t)p.S);
+        const uint32_t t = rr / (uint32_t)p.S;
+        h = (int)(t % (uint32_t)jb.H);
+        b = (int)(t / (uint32_t)jb.H);
+      }
+      const int pos = jb.rope ? table_row(PA ? row_position(p.pos, p.pos_base, p.pos0, b, s, p.S) : p.pos0 + s,
+                                          p.max_pos)
+                              : 0;
+      // destination (a cache row base or a page is a load of its own)
+      const int drow = jb.use_row_base ? ((p.row_base ? p.row_base[b] : p.row0) + s) : s;
+      int64_t slab = b, prow = drow;
       if (jb.use_row_base && p.block_table) {
-        slab = p.block_table[bb[u] * p.bt_stride + drow / p.page_size];
+        slab = p.block_table[b * p.bt_stride + drow / p.page_size];
         prow = drow % p.page_size;
       }
-      TO* dst = reinterpret_cast<TO*>(jb.dst) + slab * jb.db + hh[u] * jb.dh + prow * jb.ds + sub * 8;
-      store8<TO>(dst, x1[u]);
-      store8<TO>(dst + D / 2, x2[u]);
+      const TI* src = reinterpret_cast<const TI*>(jb.src) + b * jb.sb + h * jb.sh + s * jb.ss + sub * 8;
+      floatx8 x1 = Vec8<TI>::load_f32(src);
+      floatx8 x2 = Vec8<TI>::load_f32(src + D / 2);
+      if (jb.rope) {
+        // a position outside the tables reads row 0 and gives NaN (below)
+        const int64_t toff = (int64_t)(pos < 0 ? 0 : pos) * (D / 2) + sub * 8;
+        global_load_lds16(p.cos_tab + toff, tslot);
+        global_load_lds16(p.cos_tab + toff + 4, tslot + 1024);
+        global_load_lds16(p.sin_tab + toff, tslot + 2048);
+        global_load_lds16(p.sin_tab + toff + 4, tslot + 3072);
+      }
+      wait_vmcnt0();
+      const int z = row_opaque_zero();
+      if (jb.norm) {
+        const unsigned char* w = wslot + z + sub * 32;
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(w);
+        const floatx4 a1 = *reinterpret_cast<const floatx4*>(w + 16);
+        const floatx4 b0 = *reinterpret_cast<const floatx4*>(w + D * 2);
+        const floatx4 b1 = *reinterpret_cast<const floatx4*>(w + D * 2 + 16);
+        const floatx8 w1{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const floatx8 w2{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+        norm_row<D>(x1, x2, w1, w2, p.eps);
+      }
+      if (jb.rope) {
+        const unsigned char* t = tslot + z + lane * 16;
+        const floatx4 c0 = *reinterpret_cast<const floatx4*>(t);
+        const floatx4 c1 = *reinterpret_cast<const floatx4*>(t + 1024);
+        const floatx4 s0 = *reinterpret_cast<const floatx4*>(t + 2048);
+        const floatx4 s1 = *reinterpret_cast<const floatx4*>(t + 3072);
+        const float nan = __builtin_nanf("");
+        floatx8 c, sn;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          c[e] = pos < 0 ? nan : c0[e];
+          c[e + 4] = pos < 0 ? nan : c1[e];
+          sn[e] = pos < 0 ? nan : s0[e];
+          sn[e + 4] = pos < 0 ? nan : s1[e];
+        }
+        rope_row(x1, x2, c, sn);
+      }
+      TO* dst = reinterpret_cast<TO*>(jb.dst) + slab * jb.db + h * jb.dh + prow * jb.ds + sub * 8;
+      store8<TO>(dst, x1);
+      store8<TO>(dst + D / 2, x2);
     }
-  }
-  }
+  };
+  if (p.pos || p.pos_base) rows(std::true_type{});
+  else rows(std::false_type{});
 }
 
 template <typename TI, typename TO, int D>
 static hipError_t launch_rows(const RowParams& p, int max_h, hipStream_t st) {
-  constexpr int RPB = (64 / (D / 16)) * 4;  // rows per block and row step
+  constexpr int RPB = (64 / (D / 16)) * 4;  // rows per block and pass
+  auto kern = norm_rope_rows_kernel<TI, TO, D>;
+  // resident blocks of this instance, worked out once per device
+  static int resident[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  int cap = (dev >= 0 && dev < 64) ? __atomic_load_n(&resident[dev], __ATOMIC_RELAXED) : 0;
+  if (cap == 0) {
+    int cus = 0, per_cu = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), 256, 0);
+    if (e != hipSuccess) return e;
+    cap = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    if (dev >= 0 && dev < 64) __atomic_store_n(&resident[dev], cap, __ATOMIC_RELAXED);
+  }
   const int64_t nrows = (int64_t)p.B * max_h * p.S;
   const int64_t blocks = (nrows + RPB - 1) / RPB;
-  dim3 grid((unsigned)(blocks < ROW_MAX_BLOCKS ? blocks : ROW_MAX_BLOCKS), (unsigned)p.njobs);
-  hipLaunchKernelGGL((norm_rope_rows_kernel<TI, TO, D, 1>), grid, dim3(256), 0, st, p);
+  dim3 grid((unsigned)(blocks < cap ? blocks : cap), (unsigned)p.njobs);
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -161,6 +228,9 @@ static int qk_norm_rope_impl(const void* q, const int64_t* q_strides, void* q_ou
     return nq_fail(NQ_ERR_UNSUPPORTED, "dtype codes must be NQ_DTYPE_BF16 or NQ_DTYPE_F32");
   if ((cos_tab == nullptr) != (sin_tab == nullptr) || (cos_tab && max_pos <= 0))
     return nq_fail(NQ_ERR_INVALID, "cos and sin tables go together, with max_pos > 0");
+  // the tables and the norm weights reach LDS in 16-byte DMA pieces
+  if (!nq_aligned16(cos_tab) || !nq_aligned16(sin_tab) || !nq_aligned16(q_weight) || !nq_aligned16(k_weight))
+    return nq_fail(NQ_ERR_INVALID, "cos/sin tables and norm weights must be 16-byte aligned");
   const int esz_in = nq_dtype_size(dtype_in), esz_out = nq_dtype_size(dtype_out);
   RowParams p{};
   p.B = B; p.S = S; p.D = D; p.eps = eps;
