@@ -338,7 +338,7 @@ decode_stream_kernel(DecodeParams p) {
       for (int dq = 0; dq < NDQ; ++dq) wq[dq] = Vec8<float>::load_f32(p.qw + dq * 32 + grp * 8);
     }
     const int pos =
-        p.cos_tab ? table_row(p.q_pos ? uniform(p.q_pos[b]) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos) : 0;
+        p.cos_tab ? table_row(p.q_pos ? ld_uniform(p.q_pos, b) : (p.q_pos0 >= 0 ? p.q_pos0 : len - 1), p.max_pos) : 0;
     if (p.cos_tab) {
 #pragma unroll
       for (int dq = 0; dq < NCS; ++dq) {
