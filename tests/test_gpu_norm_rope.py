@@ -104,3 +104,42 @@ def test_rmsnorm_module_matches_oracle():
     assert_bf16_close(y, ref, "rmsnorm")
     y.float().sum().backward()  # autograd through the backward kernel
     assert norm.weight.grad is not None and torch.isfinite(norm.weight.grad).all()
+
+
+@pytest.mark.parametrize("D,S", [(32, 40000), (64, 20000), (128, 12000)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("layout", ["projections", "head_major"])
+def test_rows_many_passes_and_out_of_range_positions(D, S, dtype, layout):
+    """Enough rows that every thread of the persistent grid takes several rows, Q and K
+    jobs in one launch, rows in both enumeration orders (heads adjacent in memory, or
+    positions), explicit device positions of which some lie past the tables: those rows
+    come out NaN and every other row matches the oracle."""
+    say(f"qk_norm_rope many rows D={D} S={S} {dtype} {layout}")
+    B, Hq, Hkv, eps, max_pos = 2, 8, 4, 1e-6, S + 64
+    if layout == "projections":
+        q = randn(B, S, Hq, D, seed=31, dtype=dtype).transpose(1, 2)
+        k = randn(B, S, Hkv, D, seed=32, dtype=dtype).transpose(1, 2)
+    else:
+        q = randn(B, Hq, S, D, seed=31, dtype=dtype)
+        k = randn(B, Hkv, S, D, seed=32, dtype=dtype)
+    qw = 1 + 0.02 * randn(D, seed=33)
+    kw = 1 + 0.02 * randn(D, seed=34)
+    cos, sin = rope_tables(D, max_pos, 1e6)
+    g = torch.Generator().manual_seed(35)
+    pos = torch.randint(0, max_pos, (B, S), generator=g)
+    bad = torch.rand(B, S, generator=g) < 0.01
+    pos_dev = torch.where(bad, max_pos + 7, pos).to(torch.int32)
+    qo, ko, _ = nq.qk_norm_rope(q.to(DEV), k.to(DEV), q_weight=qw.to(DEV), k_weight=kw.to(DEV), eps=eps,
+                                cos=cos.to(DEV), sin=sin.to(DEV), position_ids=pos_dev.to(DEV))
+    torch.cuda.synchronize()
+    qo, ko = qo.cpu().float(), ko.cpu().float()
+    for name, got, x, w in (("q", qo, q, qw), ("k", ko, k, kw)):
+        nanrow = torch.isnan(got).any(-1)                     # (B, H, S)
+        assert torch.equal(nanrow, bad[:, None].expand_as(nanrow)), f"{name}: NaN rows"
+        assert torch.isnan(got[bad[:, None].expand_as(nanrow)]).all(), f"{name}: whole rows NaN"
+        want = _oracle_rows(x.float(), w, eps, cos, sin, pos)
+        ok = ~bad[:, None].expand_as(nanrow)
+        if dtype == torch.float32:
+            torch.testing.assert_close(got[ok], want[ok], rtol=2e-5, atol=2e-5)
+        else:
+            assert_bf16_close(got[ok], want[ok], name)
