@@ -61,8 +61,9 @@ def key_padding_lengths(mask: torch.Tensor, B: int, T: int) -> Optional[torch.Te
     every head and query the same prefix [0, L_b) of sequence b's keys with
     L_b >= 1 (a right-padded batch); None for any other mask (a query-dependent
     or head-dependent pattern, holes, an all-padding row, a float mask with
-    values other than 0 and -inf, or a dtype SDPA refuses), which then takes
-    SDPA itself.  The answer is cached on the mask tensor (keyed by its
+    values other than 0 and -inf, or a dtype SDPA refuses), which then runs
+    as an additive bias read by the kernels (``ops.AttnBias``, which refuses
+    what SDPA refuses).  The answer is cached on the mask tensor (keyed by its
     version), so a model that hands one mask to every layer pays one host sync.
     """
     if mask.dim() > 4 or mask.dim() == 0:
@@ -90,7 +91,7 @@ def _prefix_lengths(mask: torch.Tensor, B: int, T: int) -> Optional[torch.Tensor
         if not bool((keep | (m == float("-inf"))).all()):
             return None  # an additive bias, not a keep / drop mask
     else:
-        return None  # SDPA raises for other dtypes; let it
+        return None  # SDPA refuses other dtypes; so does AttnBias
     lens = keep.sum(-1, dtype=torch.int32)
     prefix = torch.arange(T, device=m.device)[None, :] < lens[:, None]
     if not bool(((keep == prefix).all() & (lens >= 1).all()).item()):
