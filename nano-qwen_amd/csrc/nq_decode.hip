@@ -200,9 +200,30 @@ __device__ void find_batch(const DecodeParams& p, int lane, int64_t q, int& b_ou
 __device__ __forceinline__ int64_t waves_used(const DecodeParams& p, int64_t N) {
   return p.span > 0 ? (N + p.span - 1) / p.span : min((int64_t)p.nwaves, N);
 }
-// First global step of wave w.
+// The persistent split weights the waves by the XCD they run on (workgroup i
+// runs on XCD i mod 8): a wave on an odd XCD takes DC_ODD_W / DC_EVEN_W of the
+// steps of one on an even XCD.  Timestamps per wave on MI355X put the odd XCDs'
+// waves 12-15% behind the even ones' over the same number of steps, whichever
+// rows they stream (their share of the memory system is smaller), so an even
+// split left the even XCDs idle for the last tenth of the kernel.
+constexpr int DC_EVEN_W = 25, DC_ODD_W = 22;
+// Total weight of waves [0, w).
+__device__ __forceinline__ int64_t split_weight(int64_t w) {
+  constexpr int GW = DC_WAVES * 8;  // the waves of one workgroup on each XCD
+  const int64_t rounds = w / GW;
+  const int k = (int)(w % GW), g = k / DC_WAVES, r = k % DC_WAVES;
+  return rounds * (DC_WAVES * 4) * (DC_EVEN_W + DC_ODD_W) +
+         ((int64_t)((g + 1) / 2) * DC_EVEN_W + (int64_t)(g / 2) * DC_ODD_W) * DC_WAVES +
+         (int64_t)r * ((g & 1) ? DC_ODD_W : DC_EVEN_W);
+}
+// First global step of wave w (the chunked form: span steps per wave).  The
+// weighted split applies when it still gives every wave at least one step (a
+// wave with none would leave a gap in a row's run of partials); otherwise the
+// steps are split evenly.
 __device__ __forceinline__ int64_t wave_begin(const DecodeParams& p, int64_t N, int64_t We, int64_t w) {
-  return p.span > 0 ? min(N, w * p.span) : w * N / We;
+  if (p.span > 0) return min(N, w * p.span);
+  const int64_t total = split_weight(We);
+  return N * DC_ODD_W >= total ? split_weight(w) * N / total : w * N / We;
 }
 // ---------------------------------------------------------------- kernels
 // bf16 caches (fp32 caches run the fp32 prefill kernel at S = 1)

@@ -2,7 +2,8 @@
 
 The decode kernel cuts every row (batch, kv head, head group) into 32-key steps,
 concatenates the steps of all rows and gives each wave one contiguous range of them
-(an even split over the launched waves, or `chunk/32` steps per wave).  A wave that
+(a split over the launched waves weighted by the XCD each wave runs on, or an even
+one when the weights would leave a wave without steps, or `chunk/32` steps per wave).  A wave that
 does not cover a whole row writes an fp32 partial to slot `wave + row`; the merge
 kernel combines, for each row, the partials of the waves between the first and the
 last wave that covered it (both recorded by those waves).  This test restates that
@@ -17,6 +18,17 @@ import random
 import pytest
 
 STEP = 32
+WAVES = 4                 # waves per workgroup
+EVEN_W, ODD_W = 25, 22    # persistent split: weight of a wave on an even / odd XCD
+
+
+def _split_weight(w):
+    """Total weight of waves [0, w) (workgroup i runs on XCD i mod 8)."""
+    gw = WAVES * 8
+    rounds, k = divmod(w, gw)
+    g, r = divmod(k, WAVES)
+    return (rounds * WAVES * 4 * (EVEN_W + ODD_W) + (((g + 1) // 2) * EVEN_W + (g // 2) * ODD_W) * WAVES
+            + r * (ODD_W if g & 1 else EVEN_W))
 
 
 def _steps(length, max_len):
@@ -40,7 +52,12 @@ def _check(B, Hkv, G, lens, max_len, chunk, resident=1024):
     if N == 0:
         return
     used = (N + span - 1) // span if span else min(nwaves, N)
-    begin = (lambda w: min(N, w * span)) if span else (lambda w: w * N // used)
+    if span:
+        begin = lambda w: min(N, w * span)  # noqa: E731
+    elif N * ODD_W >= _split_weight(used):  # weighted, while every wave still gets a step
+        begin = lambda w: _split_weight(w) * N // _split_weight(used)  # noqa: E731
+    else:
+        begin = lambda w: w * N // used  # noqa: E731
 
     covered = [0] * N
     slots, whole_rows, touched, first_w, last_w = {}, set(), {}, {}, {}
@@ -90,6 +107,8 @@ def _check(B, Hkv, G, lens, max_len, chunk, resident=1024):
                 n = nb[b]
                 assert n > 0
     assert all(c == 1 for c in covered)
+    if not span:  # every launched wave of the split holds at least one step
+        assert all(begin(w + 1) > begin(w) for w in range(used))
     for r in range(R):
         if nb[r // rows_per_batch] == 0:
             assert r not in touched
@@ -100,6 +119,14 @@ def _check(B, Hkv, G, lens, max_len, chunk, resident=1024):
         for w in range(wf, wl + 1):
             if wf != wl:
                 assert slots[w + r] == (w, r)
+
+
+def test_split_weights():
+    """The weights the closed form sums: waves of even workgroups EVEN_W, of odd ones ODD_W."""
+    acc = 0
+    for w in range(3 * WAVES * 8 + 5):
+        assert _split_weight(w) == acc
+        acc += ODD_W if (w // WAVES) % 2 else EVEN_W
 
 
 def test_bench_and_test_shapes():
