@@ -55,6 +55,15 @@ def _compile(src: str, obj: str, verbose: bool) -> None:
         print(out, file=sys.stderr)
 
 
+def device_asm(src: str, out: str) -> str:
+    """The gfx950 assembly hipcc makes of one .hip source, with the build's flags."""
+    cmd = [_hipcc(), *HIP_FLAGS, "--cuda-device-only", "-S", src, "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    return out
+
+
 def build(verbose: bool = False) -> str:
     """Compile every csrc/ source for gfx950 and link libnqattn.so; returns its path."""
     bdir = os.path.join(HERE, "_build")

@@ -64,7 +64,11 @@ constexpr int PF_MAX_ROWS = 256;
 constexpr int64_t PF_WIDE_MIN_WGS = 2048;  // 8-wave workgroups needed to prefer them
 constexpr int PF_BN = 64;     // keys per tile
 constexpr float PF_RESCALE_LOG2 = 8.0f;
-constexpr int PF_READ_AHEAD = 2;  // LDS operand reads in flight ahead of their MFMA
+// LDS operand reads in flight ahead of their MFMA.  They are inline asm waited
+// for by count, so no compiler-made copy or spill may touch their registers
+// before the wait: at 3 the 8-wave D = 128 instance spills a pending operand
+// (wrong results); tests/test_asm_waits.py checks the built assembly.
+constexpr int PF_READ_AHEAD = 2;
 
 // LDS reads still in flight when op i of a step's MFMA stream waits for its
 // own: those of ops i+1 .. min(i+pd, nops-1); a K operand (op < nqk) is one
