@@ -833,10 +833,19 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
     ``use_triton`` is accepted for signature compatibility (flash_attn.py:136)
     and selects nothing: the HIP kernels are the only backend, so True and
     False give the same bits.
+    head_dim 16, which the reference's kernel accepts (flash_attn.py:106), runs
+    on the head_dim-32 kernels with q, k and v zero-padded to 32: the padded
+    dimensions add exact zeros to every score and give output columns that are
+    dropped, and autograd passes through the pad and the slice.  head_dim 256
+    is refused.
     Returns a contiguous (B, H, N, D) tensor.
     """
     del use_triton
     _require_device(q, k, v)
+    if q.shape[-1] == 16 and k.shape[-1] == 16 and v.shape[-1] == 16 and q.numel() > 0:
+        scale = sm_scale if sm_scale is not None else 0.25  # 1 / sqrt(16)
+        pad = [torch.nn.functional.pad(t, (0, 16)) for t in (q, k, v)]
+        return flash_attention(*pad, causal=causal, sm_scale=scale)[..., :16].contiguous()
     if q.numel() == 0:
         # no query rows: an empty output, as the reference's grid of zero blocks gives
         return torch.empty_like(q, memory_format=torch.contiguous_format)

@@ -191,6 +191,39 @@ def test_flash_attention_mirror_autograd():
     _close_rel(v.grad, rv, "flash dv")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_attention_head_dim_16(causal):
+    """head_dim 16, which the reference's kernel accepts (kernels/flash_attn.py:106),
+    runs on the head_dim-32 kernels with zero padding: the output and the
+    gradients against fp64 autograd at D = 16 (default scale 1/4), and a
+    contiguous (B, H, N, 16) result."""
+    say(f"flash_attention D=16 causal={causal}")
+    B, H, S, D = 2, 4, 150, 16
+    q = randn(B, H, S, D, seed=551, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    k = randn(B, H, S, D, seed=552, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    v = randn(B, H, S, D, seed=553, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    do = randn(B, H, S, D, seed=554, dtype=torch.bfloat16)
+    o = nq.flash_attention(q, k, v, causal=causal)
+    assert o.shape == (B, H, S, D) and o.is_contiguous()
+    ro, rq, rk, rv = _ref_grads(q, k, v, do, causal)
+    _close_rel(o, ro, "D16 out")
+    o.backward(do.to(DEV))
+    _close_rel(q.grad, rq, "D16 dq")
+    _close_rel(k.grad, rk, "D16 dk")
+    _close_rel(v.grad, rv, "D16 dv")
+    with torch.no_grad():  # the inference path, with an explicit scale
+        o2 = nq.flash_attention(q.detach(), k.detach(), v.detach(), causal=causal, sm_scale=0.1)
+    ro2, _, _, _ = _ref_grads(q, k, v, do, causal, scale=0.1)
+    _close_rel(o2, ro2, "D16 scale")
+
+
+def test_flash_attention_head_dim_256_is_refused():
+    say("flash_attention D=256 refused")
+    q = torch.zeros(1, 2, 8, 256, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        nq.flash_attention(q, q, q, causal=True)
+
+
 def _module_grads(weights, h, g, pos, cos, sin, dtype, H, Hkv, D):
     """Oracle module forward + backward on the CPU in ``dtype`` (the reference's dtype flow)."""
     w = {n: t.detach().to(dtype).clone().requires_grad_(True) for n, t in weights.items()}
