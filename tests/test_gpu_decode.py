@@ -55,6 +55,35 @@ def test_decode_group_sizes(Hq, Hkv):
     assert_bf16_close(o, ref, f"G={Hq // Hkv}")
 
 
+@pytest.mark.parametrize("delta", [-1, 0, 1])
+def test_decode_at_the_weighted_split_threshold(delta):
+    """Total step counts N around the point where the persistent split turns to
+    the XCD weights (N * 22 >= the weight of all waves; below it the split is
+    even).  At the threshold the waves on odd XCDs take a single step each, and
+    rows are cut into the most partials the merge sees."""
+    from tests.test_decode_schedule import ODD_W, _split_weight
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    waves = min(cus * 4, 1024)  # the persistent grid: one 4-wave workgroup per CU
+    N = -(-_split_weight(waves) // ODD_W) + delta
+    say(f"decode weighted-split threshold N={N} waves={waves}")
+    B, Hq, Hkv, D = 2, 16, 1, 128
+    n0 = N // 2
+    lens = torch.tensor([n0 * 32, (N - n0) * 32 - 5], dtype=torch.int32)  # the second ends mid-step
+    Tcap = int(lens.max())
+    q = randn(B, Hq, D, seed=85, dtype=torch.bfloat16)
+    kc = randn(B, Hkv, Tcap, D, seed=86, dtype=torch.bfloat16)
+    vc = randn(B, Hkv, Tcap, D, seed=87, dtype=torch.bfloat16)
+    _poison_tail(kc, lens), _poison_tail(vc, lens)
+    qw = 1 + 0.02 * randn(D, seed=88)
+    cos, sin = rope_tables(D, Tcap, 1e6)
+    o = nq.attention_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), lens.to(DEV), max_len=Tcap,
+                            q_weight=qw.to(DEV), eps=1e-6, cos=cos.to(DEV), sin=sin.to(DEV))
+    ref = decode_path(q.float(), kc.float(), vc.float(), lens, q_weight=qw, eps=1e-6, cos=cos,
+                      sin=sin, q_pos=lens.long() - 1)
+    assert torch.isfinite(o.float().cpu()).all()
+    assert_bf16_close(o, ref, f"threshold N={N}")
+
+
 def test_split_count_does_not_change_the_result():
     say("decode split invariance")
     B, Hq, Hkv, D, Tcap = 2, 16, 2, 128, 5000
