@@ -788,7 +788,13 @@ static int prefill_entry(const void* q, const int64_t* q_strides, const void* k,
                          int Hkv, int S, int T, int D, int dtype, const float* q_weight, float eps,
                          const float* cos_tab, const float* sin_tab, int max_pos, const int32_t* q_pos,
                          const int32_t* q_pos_base, int q_pos0, int causal, float sm_scale, void* stream) {
-  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
+  // head_dim 256 (kernels/flash_attn.py:106): plain bf16 attention only
+  const bool wide = D == 256;
+  if (wide && (dtype != NQ_DTYPE_BF16 || q_weight || cos_tab || key_lens || bias || bt))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim 256 takes bf16 q/k/v without QK-Norm/RoPE fusion, key lengths, "
+                   "bias or paging");
+  if (!wide && !head_dim_ok(D))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || T <= 0)
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d S=%d T=%d)", B, Hq, Hkv, S, T);
@@ -796,7 +802,7 @@ static int prefill_entry(const void* q, const int64_t* q_strides, const void* k,
   const int G = Hq / Hkv;
   const bool f32 = dtype == NQ_DTYPE_F32;  // fp32 q, k, v, o: the fp32 MFMA kernel
   if (f32 && 128 % G) return nq_fail(NQ_ERR_UNSUPPORTED, "fp32: GQA group size %d must divide 128", G);
-  if (PF_MAX_ROWS % G) return nq_fail(NQ_ERR_UNSUPPORTED, "GQA group size %d must divide %d", G, PF_MAX_ROWS);
+  if (!wide && PF_MAX_ROWS % G) return nq_fail(NQ_ERR_UNSUPPORTED, "GQA group size %d must divide %d", G, PF_MAX_ROWS);
   if (D == 32 && 128 % G)
     return nq_fail(NQ_ERR_UNSUPPORTED, "at head_dim 32 the GQA group size %d must divide 128", G);
   if (causal && S > T) return nq_fail(NQ_ERR_INVALID, "causal attention needs S <= T (S=%d T=%d)", S, T);
@@ -842,6 +848,13 @@ static int prefill_entry(const void* q, const int64_t* q_strides, const void* k,
   p.scale_log2 = scale * kLog2e;
   const bool fuse = q_weight != nullptr || cos_tab != nullptr;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (wide) {
+    p.BM = 64;
+    p.nqb = (S + 63) / 64;
+    if ((int64_t)p.nqb * B * Hq >= (1LL << 31))
+      return nq_fail(NQ_ERR_UNSUPPORTED, "too many query blocks for one launch");
+    return nq_check_launch(launch_prefill_wide(p, causal != 0, st));
+  }
   if (f32) {
     p.BM = 128 / G;
     p.nqb = (S + p.BM - 1) / p.BM;

@@ -58,4 +58,8 @@ __device__ __forceinline__ int pf_keys(const PrefillParams& p, int b) {
 // p.BM must be 128 / G (4 waves of 32 query rows).
 hipError_t launch_prefill_f32(const PrefillParams& p, int D, bool causal, bool fuse, hipStream_t st);
 
+// Plain bf16 attention at head_dim 256 (no fusion, key lengths, bias or
+// pages); p.nqb counts 64-row query blocks.
+hipError_t launch_prefill_wide(const PrefillParams& p, bool causal, hipStream_t st);
+
 }  // namespace nq

@@ -217,10 +217,10 @@ def test_flash_attention_head_dim_16(causal):
     _close_rel(o2, ro2, "D16 scale")
 
 
-def test_flash_attention_head_dim_256_is_refused():
-    say("flash_attention D=256 refused")
-    q = torch.zeros(1, 2, 8, 256, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(RuntimeError, match="head_dim"):
+def test_flash_attention_head_dim_256_has_no_backward():
+    say("flash_attention D=256 with grad refused")
+    q = torch.zeros(1, 2, 8, 256, dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    with pytest.raises(NotImplementedError, match="256"):
         nq.flash_attention(q, q, q, causal=True)
 
 

@@ -141,6 +141,35 @@ def test_flash_attention_mirror_and_lse():
     torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-3, atol=2e-2)
 
 
+@pytest.mark.parametrize("Hq,Hkv,S,T,causal", [(4, 4, 150, 150, True), (8, 2, 77, 301, True), (2, 2, 1, 1, True),
+                                                (4, 1, 130, 130, False), (4, 2, 257, 64, False)])
+def test_head_dim_256_prefill(Hq, Hkv, S, T, causal):
+    """head_dim 256 (kernels/flash_attn.py:106 accepts it) runs on a kernel of its
+    own: the output against the oracle at the bf16 gate, the LSE against
+    logsumexp of the fp32 scores, flash_attention equal to it bit for bit, and
+    the fused options refused."""
+    say(f"prefill D=256 {Hq}/{Hkv} S={S} T={T} causal={causal}")
+    B, D = 2, 256
+    q = randn(B, Hq, S, D, seed=91, dtype=torch.bfloat16)
+    k = randn(B, Hkv, T, D, seed=92, dtype=torch.bfloat16)
+    v = randn(B, Hkv, T, D, seed=93, dtype=torch.bfloat16)
+    o, lse = nq.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, return_lse=True)
+    assert o.shape == (B, Hq, S, D)
+    ref = attention(q.float(), k.float(), v.float(), causal=causal, causal_offset=T - S)
+    assert_bf16_close(o, ref, "D=256")
+    qf = q.float().reshape(B, Hkv, Hq // Hkv, S, D)
+    s = torch.matmul(qf, k.float()[:, :, None].transpose(-1, -2)).reshape(B, Hq, S, T) / 16.0
+    if causal:
+        s = s.masked_fill(torch.ones(S, T, dtype=torch.bool).triu(T - S + 1), float("-inf"))
+    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-3, atol=2e-2)
+    if S == T and Hq == Hkv:
+        f = nq.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
+        assert f.is_contiguous() and torch.equal(f.cpu(), o.contiguous().cpu())
+    with pytest.raises(RuntimeError, match="head_dim 256"):
+        nq.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal,
+                             q_weight=torch.ones(D, device=DEV), eps=1e-6)
+
+
 def test_explicit_position_ids_and_yarn_high_positions():
     say("prefill position_ids + YaRN")
     B, S, Hq, Hkv, D = 2, 96, 8, 2, 128
