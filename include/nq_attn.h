@@ -19,9 +19,9 @@
  *     arithmetic is fp32 everywhere.
  *   - head_dim must be 32, 64 or 128 (the reference's configs use 32 and 128).
  *     kernels/flash_attn.py:106 also allows 16 and 256: nq_attn_prefill_fwd
- *     takes 256 for plain bf16 attention (no QK-Norm/RoPE fusion or key
- *     lengths; no backward); 16 is refused here with NQ_ERR_UNSUPPORTED (the
- *     Python wrapper pads it to 32).  num_heads % num_kv_heads == 0 and query
+ *     and nq_attn_bwd take 256 for plain bf16 attention (no QK-Norm/RoPE
+ *     fusion, key lengths or bias); 16 is refused here with
+ *     NQ_ERR_UNSUPPORTED (the Python wrapper pads it to 32).  num_heads % num_kv_heads == 0 and query
  *     head h reads kv head h / (num_heads / num_kv_heads).
  *   - cos/sin tables are fp32 (max_pos, head_dim/2) row-major, as built by the
  *     reference's RotaryEmbedding (plain RoPE or YaRN).  A row rotated at a

@@ -786,13 +786,19 @@ static int bwd_entry(const void* q, const int64_t* q_strides, const void* k, con
                      const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
                      int64_t workspace_bytes, int B, int Hq, int Hkv, int S, int T, int D, int dtype, int causal,
                      float sm_scale, void* stream) {
-  if (!head_dim_ok(D)) return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128, got %d", D);
+  // head_dim 256 (kernels/flash_attn.py:106): the gradient of the plain bf16 forward
+  const bool wide = D == 256;
+  if (wide && (dtype != NQ_DTYPE_BF16 || bias || key_lens))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim 256 takes bf16 tensors without key lengths or bias");
+  if (!wide && !head_dim_ok(D))
+    return nq_fail(NQ_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256, got %d", D);
   if (!nq_dtype_ok(dtype)) return nq_fail(NQ_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || T <= 0)
     return nq_fail(NQ_ERR_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d S=%d T=%d)", B, Hq, Hkv, S, T);
   if (Hq % Hkv) return nq_fail(NQ_ERR_INVALID, "num_heads %d not divisible by num_kv_heads %d", Hq, Hkv);
   const int G = Hq / Hkv;
-  if (128 % G) return nq_fail(NQ_ERR_UNSUPPORTED, "the backward needs 128 %% (Hq/Hkv) == 0, got G=%d", G);
+  if (!wide && 128 % G)
+    return nq_fail(NQ_ERR_UNSUPPORTED, "the backward needs 128 %% (Hq/Hkv) == 0, got G=%d", G);
   if (causal && S > T) return nq_fail(NQ_ERR_INVALID, "causal attention needs S <= T (S=%d T=%d)", S, T);
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   const int64_t* strs[] = {q_strides, k_strides, v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides};
@@ -859,6 +865,12 @@ static int bwd_entry(const void* q, const int64_t* q_strides, const void* k, con
   p.scale = sm_scale > 0.f ? sm_scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = p.scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (wide) {
+    p.nqb = (S + 63) / 64;
+    if ((int64_t)p.nqb * B * Hq >= (1LL << 31) || (int64_t)((T + 63) / 64) * B * Hkv >= (1LL << 31))
+      return nq_fail(NQ_ERR_UNSUPPORTED, "too many blocks for one launch");
+    return nq_check_launch(launch_bwd_wide(p, causal != 0, st));
+  }
   if (f32) return nq_check_launch(launch_bwd_f32(p, D, causal != 0, st));
   const hipError_t e =
       with_head_dim(D, [&](auto dc) { return launch_bwd<decltype(dc)::value, bf16>(p, nw, causal != 0, st); });

@@ -55,4 +55,8 @@ __device__ __forceinline__ int64_t bw_ws_index(const BwdParams& p, int b, int h,
 // The fp32 backward (every tensor fp32; products on v_mfma_f32_32x32x2_f32).
 hipError_t launch_bwd_f32(const BwdParams& p, int D, bool causal, hipStream_t st);
 
+// The head_dim 256 backward (bf16, no key lengths or bias): dQ with Delta,
+// then dK/dV; p.nqb counts 64-row query blocks.
+hipError_t launch_bwd_wide(const BwdParams& p, bool causal, hipStream_t st);
+
 }  // namespace nq

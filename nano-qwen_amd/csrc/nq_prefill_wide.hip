@@ -10,7 +10,8 @@
 // Decomposition: a workgroup of 4 waves takes 64 query rows of one head, 16
 // per wave, and walks the keys 32 at a time.  K and V tiles (32 rows x 512 B)
 // are loaded cooperatively, one step ahead into registers, and stored to LDS
-// with an XOR swizzle; every wave reads them as MFMA operands:
+// (K in the row layout, V in the tr layout of nq_wide.hpp); every wave reads
+// them as MFMA operands:
 //   S^T (keys x rows) = K Q^T on v_mfma_f32_16x16x32_bf16 (A = K from LDS,
 //   ds_read_b128; B = Q in registers, pre-scaled by sm_scale * log2 e), and
 //   O^T (dims x rows) += V^T P^T (A = V^T by transpose reads, B = P in
@@ -21,28 +22,19 @@
 #include "nq_common.hpp"
 #include "nq_internal.hpp"
 #include "nq_prefill.hpp"
+#include "nq_wide.hpp"
 
 namespace nq {
 
-constexpr int PW_D = 256;
-constexpr int PW_KEYS = 32;        // keys per step
-constexpr int PW_RB = PW_D * 2;    // bytes per K/V row
+constexpr int PW_KEYS = PW_TILE;   // keys per step
 constexpr int PW_ROWS = 64;        // query rows per workgroup (16 per wave)
-constexpr int PW_PIECES = PW_KEYS * PW_RB / 16 / 256;  // 16-byte pieces per thread per tile
-
-// Rows are 512 B, a multiple of the 256-byte bank line, so (as for 256-byte
-// rows) row r's chunks are XOR-swizzled by r: a ds_read_b128 of one chunk
-// from 16 consecutive rows (K) and a transpose read of 8 consecutive rows (V)
-// then hit distinct bank groups.
-__device__ __forceinline__ int pw_kswz(int row) { return row & 15; }
-__device__ __forceinline__ int pw_vswz(int row) { return (row & 7) * 2; }
 
 template <bool CAUSAL>
 __global__ void __launch_bounds__(256) prefill_wide_kernel(PrefillParams p) {
   constexpr int NDQ = PW_D / 32;  // 32-wide k-steps of S^T
   constexpr int NDO = PW_D / 16;  // 16-wide output blocks
-  __shared__ __attribute__((aligned(16))) unsigned char kt[PW_KEYS * PW_RB];
-  __shared__ __attribute__((aligned(16))) unsigned char vt[PW_KEYS * PW_RB];
+  __shared__ __attribute__((aligned(16))) unsigned char kt[PW_TILE_BYTES];  // row layout
+  __shared__ __attribute__((aligned(16))) unsigned char vt[PW_TILE_BYTES];  // tr layout
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -87,12 +79,6 @@ __global__ void __launch_bounds__(256) prefill_wide_kernel(PrefillParams p) {
   };
   load(0);
 
-  // K operand (A of S^T): key kb*16 + c16, logical chunk 4 dq + grp
-  const int koff = c16 * PW_RB + ((grp ^ pw_kswz(c16)) << 4);
-  // V^T operand: rows 4 grp + jj/4 (+16 for the second half), dims dd*16 + 4 (jj%4)
-  const int jj = lane & 15;
-  const int vrow = 4 * grp + (jj >> 2);
-  const int voff = vrow * PW_RB + ((pw_vswz(vrow) >> 1) << 5) + (jj & 3) * 8;
   const int lim = CAUSAL ? min(p.T - 1, row + coff) : p.T - 1;  // last key this row keeps
 
   float m_i = -INFINITY, l_i = 0.f;
@@ -105,10 +91,8 @@ __global__ void __launch_bounds__(256) prefill_wide_kernel(PrefillParams p) {
     __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
     for (int i = 0; i < PW_PIECES; ++i) {
-      const int pc = threadIdx.x + 256 * i;
-      const int r = pc >> 5, c = pc & 31;
-      *reinterpret_cast<bf16x8*>(kt + r * PW_RB + ((c ^ pw_kswz(r)) << 4)) = kr[i];
-      *reinterpret_cast<bf16x8*>(vt + r * PW_RB + ((c ^ pw_vswz(r)) << 4)) = vr[i];
+      pw_store_row(kt, threadIdx.x + 256 * i, kr[i]);
+      pw_store_tr(vt, threadIdx.x + 256 * i, vr[i]);
     }
     __syncthreads();
     if (s + 1 < nsteps) load(k0 + PW_KEYS);
@@ -118,10 +102,7 @@ __global__ void __launch_bounds__(256) prefill_wide_kernel(PrefillParams p) {
     for (int kb = 0; kb < 2; ++kb) {
       sc[kb] = floatx4{};
 #pragma unroll
-      for (int dq = 0; dq < NDQ; ++dq) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + ((koff ^ (dq << 6)) + kb * 16 * PW_RB));
-        sc[kb] = mfma16(a, qop[dq], sc[kb]);
-      }
+      for (int dq = 0; dq < NDQ; ++dq) sc[kb] = mfma16(pw_row_operand(kt, kb * 16, dq, lane), qop[dq], sc[kb]);
     }
     if (k0 + PW_KEYS - 1 > lim) {
 #pragma unroll
@@ -156,10 +137,7 @@ __global__ void __launch_bounds__(256) prefill_wide_kernel(PrefillParams p) {
 #pragma unroll
     for (int dd = 0; dd < NDO; ++dd) {
       oacc[dd] *= alpha;
-      const unsigned char* src = vt + (voff ^ (dd << 5));
-      const bf16x8 a = lds_read_tr8(reinterpret_cast<const bf16*>(src),
-                                    reinterpret_cast<const bf16*>(src + 16 * PW_RB));
-      oacc[dd] = mfma16(a, pop, oacc[dd]);
+      oacc[dd] = mfma16(pw_tr_operand(vt, dd, lane), pop, oacc[dd]);
     }
   }
 

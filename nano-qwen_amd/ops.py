@@ -837,14 +837,11 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
     on the head_dim-32 kernels with q, k and v zero-padded to 32: the padded
     dimensions add exact zeros to every score and give output columns that are
     dropped, and autograd passes through the pad and the slice.  head_dim 256
-    runs on a kernel of its own, forward only: with inputs that require grad
-    it raises NotImplementedError.
+    runs on kernels of its own, forward and backward (bf16).
     Returns a contiguous (B, H, N, D) tensor.
     """
     del use_triton
     _require_device(q, k, v)
-    if q.shape[-1] == 256 and torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
-        raise NotImplementedError("head_dim 256 has a forward kernel only; there is no backward kernel for it")
     if q.shape[-1] == 16 and k.shape[-1] == 16 and v.shape[-1] == 16 and q.numel() > 0:
         scale = sm_scale if sm_scale is not None else 0.25  # 1 / sqrt(16)
         pad = [torch.nn.functional.pad(t, (0, 16)) for t in (q, k, v)]

@@ -217,11 +217,40 @@ def test_flash_attention_head_dim_16(causal):
     _close_rel(o2, ro2, "D16 scale")
 
 
-def test_flash_attention_head_dim_256_has_no_backward():
-    say("flash_attention D=256 with grad refused")
-    q = torch.zeros(1, 2, 8, 256, dtype=torch.bfloat16, device=DEV, requires_grad=True)
-    with pytest.raises(NotImplementedError, match="256"):
-        nq.flash_attention(q, q, q, causal=True)
+@pytest.mark.parametrize("Hq,Hkv,S,T,causal", [(4, 4, 150, 150, True), (8, 2, 77, 301, True), (2, 1, 20, 20, True),
+                                                (4, 2, 130, 130, False), (4, 4, 257, 64, False)])
+def test_attention_backward_head_dim_256(Hq, Hkv, S, T, causal):
+    """head_dim 256 on its own backward kernels: dq, dk, dv against fp64 autograd;
+    GQA sums over the group, S < T and S > T, and a sequence shorter than one
+    64-row query block (its scratch holds a single 32-row tile)."""
+    say(f"bwd D=256 {Hq}/{Hkv} S={S} T={T} causal={causal}")
+    B, D = 2, 256
+    q = randn(B, Hq, S, D, seed=591, dtype=torch.bfloat16)
+    k = randn(B, Hkv, T, D, seed=592, dtype=torch.bfloat16)
+    v = randn(B, Hkv, T, D, seed=593, dtype=torch.bfloat16)
+    do = randn(B, Hq, S, D, seed=594, dtype=torch.bfloat16)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, return_lse=True)
+    dq, dk, dv = ops.attention_backward(q.to(DEV), k.to(DEV), v.to(DEV), o, do.to(DEV), lse, causal=causal)
+    _, rq, rk, rv = _ref_grads(q, k, v, do, causal)
+    _close_rel(dq, rq, "dq D=256")
+    _close_rel(dk, rk, "dk D=256")
+    _close_rel(dv, rv, "dv D=256")
+
+
+def test_flash_attention_head_dim_256_autograd():
+    say("flash_attention D=256 autograd")
+    B, H, S, D = 2, 4, 100, 256
+    q = randn(B, H, S, D, seed=601, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    k = randn(B, H, S, D, seed=602, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    v = randn(B, H, S, D, seed=603, dtype=torch.bfloat16).to(DEV).requires_grad_(True)
+    do = randn(B, H, S, D, seed=604, dtype=torch.bfloat16)
+    o = nq.flash_attention(q, k, v, causal=True)
+    o.backward(do.to(DEV))
+    ro, rq, rk, rv = _ref_grads(q, k, v, do, True)
+    _close_rel(o, ro, "D256 out")
+    _close_rel(q.grad, rq, "D256 dq")
+    _close_rel(k.grad, rk, "D256 dk")
+    _close_rel(v.grad, rv, "D256 dv")
 
 
 def _module_grads(weights, h, g, pos, cos, sin, dtype, H, Hkv, D):
