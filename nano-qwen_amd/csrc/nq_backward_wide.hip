@@ -14,8 +14,8 @@
 //   in registers), P = exp2(S - LSE), dS = P (dP - Delta), and
 //   dQ^T += K^T dS^T (A = K^T by transpose reads).
 // bwd_dkdv_wide_kernel: 4 waves x 16 keys of one kv head, K and V rows in
-//   registers.  Per 32-row query tile of each of the G heads: S^T = Q K^T and
-//   dP^T = dO V^T (rows on M: each lane holds 8 rows of one key, in the order
+//   registers.  Per 32-row query tile of each of the G heads: S = Q K^T and
+//   dP = dO V^T (rows on M: each lane holds 8 rows of one key, in the order
 //   that packs into the B operand of the next products), then
 //   dV^T += dO^T P and dK^T += Q^T dS (A = dO^T, Q^T by transpose reads).
 // dQ = scale dS K and dK = scale dS^T Q; the scores run in log2 units.
@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(256) bwd_dkdv_wide_kernel(BwdParams p) {
     __syncthreads();
     if (s + 1 < nsteps) load(s + 1);
 
-    // S^T and dP^T (rows x keys): lane holds rows 16 mb + 4 grp + i of its key
+    // S and dP (rows x keys): lane holds rows 16 mb + 4 grp + i of its key
     floatx4 st[2], dpt[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
